@@ -1,0 +1,178 @@
+/*
+ * h3mi355x.h -- C ABI of the MI355X (gfx950) MiniMax-H3 DiT hot-path library
+ * (libh3mi355x.so).
+ *
+ * The struct ABI and the entry points mirror the NineToothed HIP-AOT launchers
+ * the reference links into InfiniCore:
+ *   - `NineToothedTensor {data, shape, strides}` with strides in ELEMENTS and
+ *     scalars passed as `{&double, NULL, NULL}`: the reference fills it at
+ *     patches/InfiniCore.patch:1062-1073 (View<N>) and :1086 (eps scalar).
+ *   - `NineToothedResult launch_<kernel>(NineToothedStream stream, NineToothedTensor ...)`
+ *     with one tensor per kernel parameter in the kernel's declaration order:
+ *     emitted at patches/ninetoothed.patch:138-146 and :259-260.
+ *   - Return 0 on success, a hipError_t value otherwise; a launch whose grid
+ *     would be empty returns 0 without touching the device
+ *     (patches/ninetoothed.patch:304-307). Every launcher validates shapes,
+ *     strides and alignment on the host before any HIP call and returns
+ *     hipErrorInvalidValue (1) when they do not fit.
+ *   - The launchers allocate nothing; every buffer is owned by the caller.
+ *     They are reentrant and enqueue on the caller's stream (NULL = the
+ *     default stream).
+ *
+ * Element types are fixed per entry point (the NineToothed tensor carries no
+ * dtype): bf16 unless stated otherwise.
+ */
+#ifndef H3MI355X_H
+#define H3MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *NineToothedStream;  /* hipStream_t */
+typedef int NineToothedResult;    /* hipError_t */
+
+typedef struct NineToothedTensor {
+    void *data;
+    uint64_t *shape;
+    int64_t *strides;
+} NineToothedTensor;
+
+/* ---------------------------------------------------------------- attention */
+
+/* Non-causal full attention forward, O = softmax(Q K^T * scale) V.
+ * q, o: [B, H, Sq, 128]; k, v: [B, H, Sk, 128]; any strides on B/H/S, unit
+ * stride on the head dim, 16-byte aligned rows. Sq may differ from Sk (keys
+ * past Sk are masked). scale: fp64 scalar. fp32 logits and softmax state, bf16
+ * P for the P.V product, fp32 denominator.
+ * Replaces launch_h3_full_attention (tools/h3_attention.py:25-41,104-121;
+ * called at patches/InfiniCore.patch:1421-1422 with the [B,S,H,D] -> [B,H,S,D]
+ * stride swap of :1403-1411). */
+NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothedTensor q,
+                                           NineToothedTensor k, NineToothedTensor v,
+                                           NineToothedTensor scale, NineToothedTensor o);
+
+/* Per-head fp8 (OCP e4m3fn) quantisation for the fp8 attention variant.
+ * x: bf16 [B, H, S, 128] (any strides on B/H/S, unit stride on D);
+ * x8: uint8 storage of e4m3fn, same shape; descale: fp32 [H] (contiguous),
+ * receives amax_h / 448, the factor that maps x8 back to x. A head with
+ * amax 0 gets descale 1 and all-zero codes.
+ * No counterpart in the reference (it has no fp8 path); its callers are the
+ * fp8 attention users below. */
+NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, NineToothedTensor x,
+                                                  NineToothedTensor x8, NineToothedTensor descale);
+
+/* fp8 (OCP e4m3fn) non-causal attention forward with per-head descales.
+ * q8, k8, v8: uint8 e4m3fn [B, H, S, 128] (unit stride on D, 16-byte aligned
+ * rows); q_descale, k_descale, v_descale: fp32 [H]; scale: fp64 scalar;
+ * o: bf16 [B, H, Sq, 128]. Logits accumulate in fp32 on the fp8 MFMA; P is
+ * requantised per tile to e4m3fn with the fixed factor 448 (P <= 1 after the
+ * running-max shift); the fp32 P.V accumulator is rescaled by v_descale/448.
+ * No counterpart in the reference (fp8 attention is a new feature); same
+ * callers as launch_h3_full_attention. */
+NineToothedResult launch_h3_full_attention_fp8(NineToothedStream stream, NineToothedTensor q8,
+                                               NineToothedTensor k8, NineToothedTensor v8,
+                                               NineToothedTensor q_descale, NineToothedTensor k_descale,
+                                               NineToothedTensor v_descale, NineToothedTensor scale,
+                                               NineToothedTensor o);
+
+/* ---------------------------------------------------------------- pointwise */
+
+/* out = bf16(up * bf16(g / (1 + exp(-g)))), g = fp32(gate). [B, S, F], any
+ * strides. Replaces launch_h3_swiglu_exact (tools/h3_pointwise.py:9-34; called
+ * at patches/InfiniCore.patch:1101). */
+NineToothedResult launch_h3_swiglu_exact(NineToothedStream stream, NineToothedTensor up,
+                                         NineToothedTensor gate, NineToothedTensor out);
+
+/* RMSNorm with every intermediate rounded to bf16 (tools/h3_pointwise.py:46-57):
+ * x, out [B, S, W]; weight [W]; eps fp64 scalar. The _128 and _5376 entry
+ * points are the reference's width-specialised launchers
+ * (tools/h3_pointwise.py:60-70; called at patches/InfiniCore.patch:1087-1089)
+ * and require that width; launch_h3_rms_exact accepts any width. */
+NineToothedResult launch_h3_rms_exact(NineToothedStream stream, NineToothedTensor x,
+                                      NineToothedTensor weight, NineToothedTensor eps,
+                                      NineToothedTensor out);
+NineToothedResult launch_h3_rms_exact_128(NineToothedStream stream, NineToothedTensor x,
+                                          NineToothedTensor weight, NineToothedTensor eps,
+                                          NineToothedTensor out);
+NineToothedResult launch_h3_rms_exact_5376(NineToothedStream stream, NineToothedTensor x,
+                                           NineToothedTensor weight, NineToothedTensor eps,
+                                           NineToothedTensor out);
+
+/* RMSNorm + AdaLN: out = bf16(bf16(bf16(rms(x) * w) * bf16(1 + scale)) + shift).
+ * x, scale, shift, out [B, S, W] (scale/shift may broadcast with stride 0);
+ * weight [W]; eps fp64. Replaces launch_h3_rms_modulate_exact
+ * (tools/h3_pointwise.py:73-108; called at patches/InfiniCore.patch:1117-1118),
+ * width-generic. */
+NineToothedResult launch_h3_rms_modulate_exact(NineToothedStream stream, NineToothedTensor x,
+                                               NineToothedTensor weight, NineToothedTensor eps,
+                                               NineToothedTensor scale, NineToothedTensor shift,
+                                               NineToothedTensor out);
+
+/* 3-axis NeoX RoPE on channels 0..95 of [S, H, 128] (rotate-half pairs i,
+ * i+48; channels 96..127 pass through); cos/sin [S, 48] indexed by dim 0.
+ * x0/x1/xp and y0/y1/yp are the same views passed three times, as the
+ * reference's callers do. Replaces launch_h3_rope_exact
+ * (tools/h3_pointwise.py:184-231; called at patches/InfiniCore.patch:1131). */
+NineToothedResult launch_h3_rope_exact(NineToothedStream stream, NineToothedTensor x0,
+                                       NineToothedTensor x1, NineToothedTensor xp,
+                                       NineToothedTensor cos, NineToothedTensor sin,
+                                       NineToothedTensor y0, NineToothedTensor y1,
+                                       NineToothedTensor yp);
+
+/* out = bf16(x + bf16(gate * y)), [B, S, W], any strides (gate typically
+ * broadcast). Replaces launch_h3_gated_residual_exact
+ * (tools/h3_pointwise.py:112-136; called at patches/InfiniCore.patch:1144). */
+NineToothedResult launch_h3_gated_residual_exact(NineToothedStream stream, NineToothedTensor x,
+                                                 NineToothedTensor gate, NineToothedTensor y,
+                                                 NineToothedTensor out);
+
+/* residual = bf16(x + bf16(gate * y)); out = rms_modulate(residual).
+ * Replaces launch_h3_gated_residual_rms_modulate_exact
+ * (tools/h3_pointwise.py:139-182; called at patches/InfiniCore.patch:1161-1163),
+ * width-generic. */
+NineToothedResult launch_h3_gated_residual_rms_modulate_exact(
+    NineToothedStream stream, NineToothedTensor x, NineToothedTensor gate, NineToothedTensor y,
+    NineToothedTensor weight, NineToothedTensor eps, NineToothedTensor scale,
+    NineToothedTensor shift, NineToothedTensor residual, NineToothedTensor out);
+
+/* Per-(token, head) RMSNorm over 128 channels (weight [128]) then the
+ * rotate-half RoPE of launch_h3_rope_exact, on x [T, P, Hs, 128] (any strides)
+ * written to out [T, P, Hs, 128] (any strides, e.g. a permuted all-to-all send
+ * buffer); cos/sin [T, 48]. Views repeated as in the reference.
+ * Replaces launch_h3_qk_norm_rope (tools/h3_pointwise.py:234-294,370-402;
+ * called at patches/InfiniCore.patch:1180-1182). */
+NineToothedResult launch_h3_qk_norm_rope(NineToothedStream stream, NineToothedTensor x0,
+                                         NineToothedTensor x1, NineToothedTensor xp,
+                                         NineToothedTensor w0, NineToothedTensor w1,
+                                         NineToothedTensor wp, NineToothedTensor eps,
+                                         NineToothedTensor cos, NineToothedTensor sin,
+                                         NineToothedTensor y0, NineToothedTensor y1,
+                                         NineToothedTensor yp);
+
+/* The same RMSNorm followed by an interleaved-pair RoPE over all 128
+ * channels: pair i = channels (2i, 2i+1), angle table cos/sin [T, 64]
+ * (rotary channels split 32/48/48 over the t/h/w axes). Per-step bf16
+ * rounding as launch_h3_qk_norm_rope. No counterpart in the reference (its
+ * table is rotate-half over 96 channels, tools/h3_pointwise.py:184-214); it
+ * serves callers whose RoPE uses the interleaved 32/48/48 layout. */
+NineToothedResult launch_h3_qk_norm_rope_interleaved(NineToothedStream stream, NineToothedTensor x,
+                                                     NineToothedTensor weight, NineToothedTensor eps,
+                                                     NineToothedTensor cos, NineToothedTensor sin,
+                                                     NineToothedTensor out);
+
+/* H3's RoPE table: cos/sin[t, a*16 + k] = bf16(cos/sin(fp32(position[t, a]) *
+ * (1 / power[k]))), position fp64 [T, 3], power fp32 [16], cos/sin bf16
+ * [T, 48] views (the halves of a [T, 96] cache). Replaces launch_h3_rope_cache
+ * (tools/h3_pointwise.py:405-442; called at patches/InfiniCore.patch:1197). */
+NineToothedResult launch_h3_rope_cache(NineToothedStream stream, NineToothedTensor position,
+                                       NineToothedTensor power, NineToothedTensor cos,
+                                       NineToothedTensor sin);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3MI355X_H */

@@ -1,0 +1,24 @@
+"""MI355X (gfx950) implementation of MiniMax-H3's DiT hot path: non-causal
+full-sequence attention (bf16, and an fp8 e4m3fn variant) and the fused
+pointwise ops around it, as hand-written HIP kernels behind the C ABI of
+include/h3mi355x.h (libh3mi355x.so).
+
+The Python faces mirror the reference's factories: `h3_attention.make_attention`
+and the `h3_pointwise.make_*` functions. The package name is not a Python
+identifier; import it with importlib.import_module("minimaxh3_on_k100-ai_amd").
+"""
+from . import _lib, h3_attention, h3_pointwise  # noqa: F401
+from .h3_attention import make_attention, make_attention_fp8, quantize_fp8_per_head  # noqa: F401
+from .h3_pointwise import (  # noqa: F401
+    make_gated_residual,
+    make_gated_residual_rms_modulate,
+    make_qk_norm_rope,
+    make_qk_norm_rope_interleaved,
+    make_rms,
+    make_rms_modulate,
+    make_rope,
+    make_rope_cache,
+    make_swiglu,
+)
+
+library = _lib.library

@@ -1,0 +1,70 @@
+"""Build recipe for libh3mi355x.so: every csrc/*.hip compiled for gfx950 with
+hipcc, linked into one shared library next to this file.
+
+    python -m <package>._build        (or __graft_entry__.build())
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC = PACKAGE_DIR / "csrc"
+BUILD_DIR = PACKAGE_DIR / "_build"
+LIBRARY = PACKAGE_DIR / "libh3mi355x.so"
+ARCH = "gfx950"
+
+# -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (some of
+# their forms have given silently wrong results on these boxes).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-flush-denormals-to-zero", "-ffp-contract=off",
+]
+
+
+def hipcc() -> str:
+    found = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists() and not shutil.which(found):
+        raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
+    return found
+
+
+def _compile(source: Path) -> Path:
+    obj = BUILD_DIR / (source.stem + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, "-c", str(source), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {source.name}:\n{stderr}")
+    if stderr.strip():
+        print(stderr, file=sys.stderr)
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every HIP source and link libh3mi355x.so (always rebuilds)."""
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    BUILD_DIR.mkdir(exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
+        objects = list(pool.map(_compile, sources))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY} from {len(sources)} sources")
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build()

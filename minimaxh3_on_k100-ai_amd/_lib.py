@@ -1,0 +1,156 @@
+"""ctypes binding to libh3mi355x.so (the C ABI declared in include/h3mi355x.h).
+
+Tensors cross the boundary as NineToothedTensor {data, shape, strides} with
+element strides, scalars as {&double, NULL, NULL}, and every launch goes to the
+current torch stream of the tensors' device, mirroring how the reference's
+InfiniCore launchers fill the struct (patches/InfiniCore.patch:1062-1089).
+There is no fallback: a missing library or a non-zero status raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Sequence
+
+import torch
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libh3mi355x.so"
+
+# Entry points and their NineToothedTensor argument counts (stream excluded).
+ENTRY_POINTS = {
+    "launch_h3_full_attention": 5,
+    "launch_h3_full_attention_fp8": 8,
+    "launch_h3_quantize_fp8_per_head": 3,
+    "launch_h3_swiglu_exact": 3,
+    "launch_h3_rms_exact": 4,
+    "launch_h3_rms_exact_128": 4,
+    "launch_h3_rms_exact_5376": 4,
+    "launch_h3_rms_modulate_exact": 6,
+    "launch_h3_rope_exact": 8,
+    "launch_h3_gated_residual_exact": 4,
+    "launch_h3_gated_residual_rms_modulate_exact": 9,
+    "launch_h3_qk_norm_rope": 12,
+    "launch_h3_qk_norm_rope_interleaved": 6,
+    "launch_h3_rope_cache": 4,
+}
+
+HIP_ERROR_INVALID_VALUE = 1
+
+
+class NineToothedTensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p),
+                ("shape", ctypes.POINTER(ctypes.c_uint64)),
+                ("strides", ctypes.POINTER(ctypes.c_int64))]
+
+
+class LaunchError(RuntimeError):
+    """A launcher returned a non-zero hipError_t."""
+
+    def __init__(self, name: str, status: int):
+        self.status = status
+        super().__init__(f"{name} failed with hipError {status} ({_error_string(status)})")
+
+
+_lib = None
+_hip = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded libh3mi355x.so; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY_PATH.exists():
+            raise ImportError(f"{LIBRARY_PATH} is missing: build it with __graft_entry__.build() "
+                              "(hipcc --offload-arch=gfx950); there is no non-HIP fallback")
+        _lib = ctypes.CDLL(str(LIBRARY_PATH))
+    return _lib
+
+
+_bound: dict = {}
+
+
+def entry(name: str):
+    """The typed ctypes function for an entry point (AttributeError if the
+    library does not export it)."""
+    fn = _bound.get(name)
+    if fn is None:
+        fn = getattr(library(), name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * ENTRY_POINTS[name]
+        _bound[name] = fn
+    return fn
+
+
+def _error_string(status: int) -> str:
+    global _hip
+    try:
+        if _hip is None:
+            _hip = ctypes.CDLL("libamdhip64.so")
+            _hip.hipGetErrorString.restype = ctypes.c_char_p
+            _hip.hipGetErrorString.argtypes = [ctypes.c_int]
+        return _hip.hipGetErrorString(status).decode()
+    except OSError:
+        return "unknown"
+
+
+class _Arg:
+    """Owns the shape/stride arrays behind one NineToothedTensor."""
+
+    __slots__ = ("struct", "_keep")
+
+    def __init__(self, data: int, shape: Sequence[int], strides: Sequence[int] | None, keep=None):
+        if strides is None:
+            self._keep = (ctypes.c_double(0.0), keep)
+            self.struct = NineToothedTensor(data, None, None)
+            return
+        n = len(shape)
+        shape_arr = (ctypes.c_uint64 * max(n, 1))(*shape)
+        stride_arr = (ctypes.c_int64 * max(n, 1))(*strides)
+        self._keep = (shape_arr, stride_arr, keep)
+        self.struct = NineToothedTensor(data, shape_arr, stride_arr)
+
+
+def tensor(t: torch.Tensor) -> _Arg:
+    return _Arg(t.data_ptr(), tuple(t.shape), tuple(t.stride()), keep=t)
+
+
+def scalar(value: float) -> _Arg:
+    box = ctypes.c_double(float(value))
+    arg = _Arg(ctypes.addressof(box), (), None, keep=box)
+    return arg
+
+
+def raw_tensor(data: int, shape: Sequence[int], strides: Sequence[int]) -> _Arg:
+    """A NineToothedTensor over raw memory (host-side validation tests)."""
+    return _Arg(data, shape, strides)
+
+
+def call(name: str, stream: int, *args: _Arg) -> int:
+    """Calls an entry point and returns its status (no exception)."""
+    return entry(name)(ctypes.c_void_p(stream), *(a.struct for a in args))
+
+
+def launch(name: str, device: torch.device, *args: _Arg) -> None:
+    """Calls an entry point on the current stream of `device`; raises on error."""
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        status = call(name, stream, *args)
+    if status != 0:
+        raise LaunchError(name, status)
+
+
+def check_cuda(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one GPU; returns that device."""
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise ValueError("H3 kernels run on the GPU: tensors must be on a cuda device")
+    for t in tensors[1:]:
+        if t.device != device:
+            raise ValueError(f"all tensors must be on {device}, got {t.device}")
+    return device
+
+
+def check_dtype(dtype: torch.dtype, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.dtype != dtype:
+            raise ValueError(f"expected {dtype}, got {t.dtype}")

@@ -1,0 +1,331 @@
+// Non-causal full attention forward for gfx950 (CDNA4), bf16 in/out, fp32
+// softmax state: the MI355X counterpart of the reference's NineToothed kernel
+// (tools/h3_attention.py:25-41, `fp32_qk` numerics).
+//
+// Work decomposition
+//   - one 256-thread workgroup per (batch, head, 256-query block); the
+//     workgroup order is remapped so the blocks dispatched to one XCD are
+//     consecutive (same head), sharing that XCD's L2 for the K/V stream;
+//   - each wave owns 64 queries as two 32-query MFMA blocks and keeps its Q^T
+//     operands in registers for the whole key loop;
+//   - K/V tiles of 64 keys are staged in double-buffered LDS.
+//
+// MFMA formulation (v_mfma_f32_32x32x16_bf16; A row = lane % 32, B column =
+// lane % 32, accumulator register i of lane l holds row 8*(i/4) + 4*(l/32) + i%4)
+//   - S^T = K Q^T: A = 32 keys x 16 dims of K from LDS, B = Q^T from registers.
+//     Each lane therefore accumulates the scores of ONE query (its column), so
+//     the softmax max/sum are per-lane plus one exchange with lane l^32.
+//   - The A operand reads K row pi(m) for MFMA row m, pi swapping bits 2 and 3.
+//     With that, accumulator register i of lane l holds key
+//     16*(i/8) + 8*(l/32) + i%8 of its 32-key block, which is exactly the
+//     B-operand layout (k = 8*(l/32) + j) of the next product:
+//   - O^T += V^T P^T: A = 32 dims x 16 keys of V^T, read from the row-major V
+//     tile with ds_read_b64_tr_b16; B = the bf16-rounded P^T registers. The
+//     O^T accumulators of a lane again belong to its own query, so the online
+//     rescale is a per-lane scalar.
+// Numerics follow the reference: fp32 logits scaled by scale*log2(e), exp2
+// online softmax, bf16 P in the P.V product, fp32 P in the denominator, fp32
+// accumulation, o = acc / denominator rounded to bf16.
+#include "h3_common.hpp"
+
+namespace h3 {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+constexpr int kD = 128;           // head dim
+constexpr int kBM = 256;          // queries per workgroup
+constexpr int kWaves = 4;
+constexpr int kBN = 64;           // keys per tile
+constexpr int kRow = kD + 8;      // LDS row pitch in elements (16-byte pad)
+constexpr int kTileElems = kBN * kRow;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+    const bf16_t *q, *k, *v;
+    bf16_t *o;
+    int64_t qs[3], ks[3], vs[3], os[3];  // element strides of B, H, S (D is unit-stride)
+    int B, H, Sq, Sk;
+    int qblocks;                          // ceil(Sq / kBM)
+    float c;                              // scale * log2(e)
+};
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// Maps the hardware workgroup id to a logical one so that each XCD (ids
+// dispatched round-robin over 8 XCDs) receives a contiguous logical range.
+__device__ __forceinline__ int xcd_remap(int x, int total) {
+    const int per = total / 8, rem = total % 8;
+    const int xcd = x % 8, slot = x / 8;
+    return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+// Global -> registers for one 64-key tile of K or V: thread t loads rows
+// t/16 + 16r (r = 0..3), 16-byte chunk t%16. Rows past `valid` are zero.
+__device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid, uint4 reg[4]) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = t / 16 + 16 * r;
+        if (row < valid) {
+            reg[r] = *reinterpret_cast<const uint4 *>(base + static_cast<int64_t>(key0 + row) * s_stride + (t % 16) * 8);
+        } else {
+            reg[r] = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ void store_tile(bf16_t *lds, const uint4 reg[4]) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) *reinterpret_cast<uint4 *>(lds + (t / 16 + 16 * r) * kRow + (t % 16) * 8) = reg[r];
+}
+
+template <bool NEG>
+__global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_fwd_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElems];
+    __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElems];
+
+    const int total = a.B * a.H * a.qblocks;
+    const int logical = xcd_remap(blockIdx.x, total);
+    const int qb = logical % a.qblocks;
+    const int bh = logical / a.qblocks;
+    const int b = bh / a.H, h = bh % a.H;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int l32 = lane & 31;
+    const int half = lane >> 5;
+
+    const bf16_t *qbase = a.q + b * a.qs[0] + h * a.qs[1];
+    const bf16_t *kbase = a.k + b * a.ks[0] + h * a.ks[1];
+    const bf16_t *vbase = a.v + b * a.vs[0] + h * a.vs[1];
+    bf16_t *obase = a.o + b * a.os[0] + h * a.os[1];
+
+    // Q^T operands: query block qs (0/1) of this wave, k-step kk covers dims
+    // 16kk + 8*half .. +8.
+    const int q_first = qb * kBM + wave * 64;
+    bf16x8_t qreg[2][8];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        int query = q_first + qs * 32 + l32;
+        query = query < a.Sq ? query : a.Sq - 1;
+        const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2] + 8 * half;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) qreg[qs][kk] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 16 * kk));
+    }
+
+    f32x16_t acc[4][2];  // O^T: dim block db (32 dims) x query block qs
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[db][qs][i] = 0.0f;
+    float m_run[2] = {-INFINITY, -INFINITY};  // running max of the logits
+    float l_run[2] = {0.0f, 0.0f};            // running denominator
+
+    const int ntiles = (a.Sk + kBN - 1) / kBN;
+    uint4 kreg[4], vreg[4];
+    load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
+    load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+    store_tile(lds_k[0], kreg);
+    store_tile(lds_v[0], vreg);
+    __syncthreads();
+
+    // K row read by MFMA row m (bits 2 and 3 swapped).
+    const int krow = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    // ds_read_b64_tr_b16 addressing for the V^T operand: within each 16-lane
+    // group, lane s points at row (s/4) and dims 4*(s%4) of its 4x16 block.
+    const int g16 = lane >> 4, s16 = lane & 15;
+    const int v_row_off = 8 * (g16 >> 1) + (s16 >> 2);
+    const int v_col_off = 16 * (g16 & 1) + 4 * (s16 & 3);
+
+    for (int tile = 0; tile < ntiles; ++tile) {
+        const int buf = tile & 1;
+        const int key0 = tile * kBN;
+        const bool has_next = tile + 1 < ntiles;
+        if (has_next) {
+            const int nvalid = a.Sk - key0 - kBN < kBN ? a.Sk - key0 - kBN : kBN;
+            load_tile(kbase, a.ks[2], key0 + kBN, nvalid, kreg);
+            load_tile(vbase, a.vs[2], key0 + kBN, nvalid, vreg);
+        }
+        const bf16_t *kt = lds_k[buf];
+        const bf16_t *vt = lds_v[buf];
+
+        // ---- S^T = K Q^T for 2 key blocks x 2 query blocks
+        f32x16_t s[2][2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[ks][qs][i] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const bf16x8_t kop =
+                    as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRow + 16 * kk + 8 * half));
+#pragma unroll
+                for (int qs = 0; qs < 2; ++qs)
+                    s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
+            }
+        }
+
+        // ---- online softmax, per lane (= per query), per query block
+        const int valid = a.Sk - key0;  // keys of this tile that exist (>= 1)
+        bf16x8_t pop[2][4];             // P^T operands: query block x 16-key step
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+            if (valid < kBN) {
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = 32 * ks + 16 * (i / 8) + 8 * half + (i % 8);
+                        if (key >= valid) s[ks][qs][i] = NEG ? INFINITY : -INFINITY;
+                    }
+            }
+            float mx = s[0][qs][0];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][qs][i]) : fmaxf(mx, s[ks][qs][i]);
+            {
+                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
+                mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
+            }
+            const float m_new = fmaxf(m_run[qs], mx * a.c);  // running max in logit units
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_new);
+            m_run[qs] = m_new;
+            float rowsum = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][qs][i], a.c, -m_new));
+                    if (valid < kBN) {
+                        const int key = 32 * ks + 16 * (i / 8) + 8 * half + (i % 8);
+                        if (key >= valid) p = 0.0f;
+                    }
+                    s[ks][qs][i] = p;
+                    rowsum += p;
+                }
+            }
+            {
+                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
+                rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            }
+            l_run[qs] = l_run[qs] * alpha + rowsum;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[db][qs][i] *= alpha;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int ks = t >> 1, base = 8 * (t & 1);
+                uint4 packed;
+                packed.x = pack2(s[ks][qs][base + 0], s[ks][qs][base + 1]);
+                packed.y = pack2(s[ks][qs][base + 2], s[ks][qs][base + 3]);
+                packed.z = pack2(s[ks][qs][base + 4], s[ks][qs][base + 5]);
+                packed.w = pack2(s[ks][qs][base + 6], s[ks][qs][base + 7]);
+                pop[qs][t] = as_bf16x8(packed);
+            }
+        }
+
+        // ---- O^T += V^T P^T
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16_t *vp = vt + (16 * t + v_row_off) * kRow + 32 * db + v_col_off;
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp));
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRow));
+                uint4 vv;
+                vv.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
+                vv.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
+                vv.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
+                vv.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+                const bf16x8_t vop = as_bf16x8(vv);
+#pragma unroll
+                for (int qs = 0; qs < 2; ++qs)
+                    acc[db][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop[qs][t], acc[db][qs], 0, 0, 0);
+            }
+        }
+
+        if (has_next) {
+            store_tile(lds_k[buf ^ 1], kreg);
+            store_tile(lds_v[buf ^ 1], vreg);
+        }
+        __syncthreads();
+    }
+
+    // ---- o = acc / denominator, bf16; lane owns one query, dims
+    // 32db + 8g + 4*half + 0..3 for g = 0..3.
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int query = q_first + qs * 32 + l32;
+        if (query >= a.Sq) continue;
+        const float inv = __fdiv_rn(1.0f, l_run[qs]);
+        bf16_t *orow = obase + static_cast<int64_t>(query) * a.os[2];
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint2 w;
+                w.x = pack2(acc[db][qs][4 * g + 0] * inv, acc[db][qs][4 * g + 1] * inv);
+                w.y = pack2(acc[db][qs][4 * g + 2] * inv, acc[db][qs][4 * g + 3] * inv);
+                *reinterpret_cast<uint2 *>(orow + 32 * db + 8 * g + 4 * half) = w;
+            }
+    }
+}
+
+}  // namespace
+}  // namespace h3
+
+using namespace h3;
+
+extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothedTensor q,
+                                                      NineToothedTensor k, NineToothedTensor v,
+                                                      NineToothedTensor scale, NineToothedTensor o) {
+    View<4> qv, kv, vv, ov;
+    double sc;
+    if (!load_view(q, 2, qv) || !load_view(k, 2, kv) || !load_view(v, 2, vv) || !load_view(o, 2, ov) ||
+        !load_scalar(scale, sc))
+        return kInvalid;
+    // Contract of the reference operator (patches/InfiniCore.patch:1366-1376):
+    // same B/H/D, q and o alike, k and v alike, Sq and Sk free; here D = 128.
+    if (!same_shape(qv, ov) || !same_shape(kv, vv)) return kInvalid;
+    if (qv.shape[0] != kv.shape[0] || qv.shape[1] != kv.shape[1] || qv.shape[3] != kv.shape[3]) return kInvalid;
+    if (qv.shape[3] != kD) return kInvalid;
+    if (!rows_vec16(qv, 2) || !rows_vec16(kv, 2) || !rows_vec16(vv, 2) || !rows_vec16(ov, 2)) return kInvalid;
+    if (qv.shape[0] == 0 || qv.shape[1] == 0 || qv.shape[2] == 0) return 0;
+    if (kv.shape[2] == 0) return kInvalid;  // softmax over no keys is undefined
+    AttnArgs a{};
+    a.q = reinterpret_cast<const bf16_t *>(qv.data);
+    a.k = reinterpret_cast<const bf16_t *>(kv.data);
+    a.v = reinterpret_cast<const bf16_t *>(vv.data);
+    a.o = reinterpret_cast<bf16_t *>(ov.data);
+    for (int i = 0; i < 3; ++i) {
+        a.qs[i] = qv.stride[i];
+        a.ks[i] = kv.stride[i];
+        a.vs[i] = vv.stride[i];
+        a.os[i] = ov.stride[i];
+    }
+    a.B = static_cast<int>(qv.shape[0]);
+    a.H = static_cast<int>(qv.shape[1]);
+    a.Sq = static_cast<int>(qv.shape[2]);
+    a.Sk = static_cast<int>(kv.shape[2]);
+    a.qblocks = (a.Sq + kBM - 1) / kBM;
+    const int64_t grid = static_cast<int64_t>(a.B) * a.H * a.qblocks;
+    if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
+    a.c = static_cast<float>(static_cast<float>(sc) * kLog2e);
+    if (a.c < 0.0f)
+        attention_fwd_kernel<true><<<static_cast<unsigned>(grid), kBM, 0, as_stream(stream)>>>(a);
+    else
+        attention_fwd_kernel<false><<<static_cast<unsigned>(grid), kBM, 0, as_stream(stream)>>>(a);
+    return launch_status();
+}

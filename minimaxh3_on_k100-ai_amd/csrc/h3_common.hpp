@@ -1,0 +1,140 @@
+// Shared host/device helpers for the gfx950 H3 hot-path kernels: the
+// NineToothedTensor view, host-side validation, and the bf16 rounding
+// primitives every kernel uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <limits>
+
+#include "../../include/h3mi355x.h"
+
+namespace h3 {
+
+// ------------------------------------------------------------------ host side
+
+constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
+
+// A validated, fixed-rank copy of a NineToothedTensor: the launchers read the
+// caller's shape/stride arrays exactly once, here.
+template <int N>
+struct View {
+    char *data = nullptr;
+    int64_t shape[N] = {};
+    int64_t stride[N] = {};
+    int64_t numel() const {
+        int64_t n = 1;
+        for (int i = 0; i < N; ++i) n *= shape[i];
+        return n;
+    }
+};
+
+// Copies `t` into `v` and checks what every tensor argument must satisfy:
+// shape/stride arrays present, sizes representable, data present unless the
+// tensor is empty. `elem` is the element size in bytes.
+template <int N>
+inline bool load_view(const NineToothedTensor &t, int elem, View<N> &v) {
+    if (t.shape == nullptr || t.strides == nullptr) return false;
+    for (int i = 0; i < N; ++i) {
+        if (t.shape[i] > static_cast<uint64_t>(std::numeric_limits<int32_t>::max())) return false;
+        v.shape[i] = static_cast<int64_t>(t.shape[i]);
+        v.stride[i] = t.strides[i];
+    }
+    v.data = static_cast<char *>(t.data);
+    if (v.numel() != 0 && v.data == nullptr) return false;
+    // The furthest element reachable must have a representable byte offset.
+    __int128 span = 0;
+    for (int i = 0; i < N; ++i) {
+        if (v.shape[i] == 0) return true;
+        __int128 s = static_cast<__int128>(v.stride[i]) * (v.shape[i] - 1);
+        span += s < 0 ? -s : s;
+    }
+    return span * elem < (static_cast<__int128>(1) << 62);
+}
+
+// Reads a NineToothed scalar ({&double, NULL, NULL}).
+inline bool load_scalar(const NineToothedTensor &t, double &out) {
+    if (t.data == nullptr) return false;
+    out = *static_cast<const double *>(t.data);
+    return true;
+}
+
+template <int N>
+inline bool same_shape(const View<N> &a, const View<N> &b) {
+    for (int i = 0; i < N; ++i)
+        if (a.shape[i] != b.shape[i]) return false;
+    return true;
+}
+
+// True when the innermost dimension is unit-stride and every row start is
+// 16-byte aligned, so the row can be streamed with 16-byte vector accesses.
+template <int N>
+inline bool rows_vec16(const View<N> &v, int elem) {
+    if (v.shape[N - 1] > 1 && v.stride[N - 1] != 1) return false;
+    if ((reinterpret_cast<uintptr_t>(v.data) & 15) != 0) return false;
+    if ((v.shape[N - 1] * elem) % 16 != 0) return false;
+    for (int i = 0; i < N - 1; ++i)
+        if (v.shape[i] > 1 && (v.stride[i] * elem) % 16 != 0) return false;
+    return true;
+}
+
+inline hipStream_t as_stream(NineToothedStream s) { return static_cast<hipStream_t>(s); }
+
+// Launch epilogue shared by all launchers: the launch status of the kernel.
+inline int launch_status() { return static_cast<int>(hipGetLastError()); }
+
+// ---------------------------------------------------------------- device side
+
+typedef uint16_t bf16_t;  // raw bf16 bits
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+// Low / high bf16 of a packed dword, widened to fp32 (exact).
+__device__ __forceinline__ float lo2f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi2f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round two fp32 values to bf16 (round-to-nearest-even, v_cvt_pk_bf16_f32) and
+// pack them, `a` in the low half.
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    f32x2_t f = {a, b};
+    bf16x2_t h = __builtin_convertvector(f, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// fp32 -> bf16 -> fp32, i.e. the value `.to(bfloat16)` leaves behind.
+__device__ __forceinline__ float rbf(float a) {
+    return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) << 16);
+}
+
+// Round a pair to bf16 and widen back (one packed conversion).
+__device__ __forceinline__ void rbf2(float &a, float &b) {
+    uint32_t p = pack2(a, b);
+    a = lo2f(p);
+    b = hi2f(p);
+}
+
+// 1/sqrt(v) with two IEEE roundings (correctly rounded sqrt, then correctly
+// rounded division): the value torch computes for rsqrt on the CPU.
+__device__ __forceinline__ float rsqrt_ieee(float v) { return __fdiv_rn(1.0f, __fsqrt_rn(v)); }
+
+struct U4 {
+    uint32_t x, y, z, w;
+};
+__device__ __forceinline__ U4 ld16(const void *p) {
+    uint4 v = *static_cast<const uint4 *>(p);
+    return {v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st16(void *p, const U4 &v) {
+    *static_cast<uint4 *>(p) = make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void u4_to_f8(const U4 &v, float f[8]) {
+    f[0] = lo2f(v.x); f[1] = hi2f(v.x); f[2] = lo2f(v.y); f[3] = hi2f(v.y);
+    f[4] = lo2f(v.z); f[5] = hi2f(v.z); f[6] = lo2f(v.w); f[7] = hi2f(v.w);
+}
+__device__ __forceinline__ U4 f8_to_u4(const float f[8]) {
+    return {pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7])};
+}
+
+}  // namespace h3

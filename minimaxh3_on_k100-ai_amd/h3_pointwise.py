@@ -1,0 +1,198 @@
+"""H3 pointwise ops with the reference's per-step bf16 rounding, on gfx950.
+
+Drop-in for tools/h3_pointwise.py: the same `make_*` factories, keyword
+arguments and returned-callable argument orders. Outputs are preallocated by the
+caller; each call enqueues one kernel of libh3mi355x.so on the current torch
+stream and returns None. Tile keywords of the reference (rows, cols, block,
+num_warps, block_tokens, ranks) are accepted for signature compatibility; the
+gfx950 kernels choose their own launch shapes, and the results do not depend
+on them.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "make_swiglu", "make_rms", "make_rms_modulate", "make_gated_residual",
+    "make_gated_residual_rms_modulate", "make_rope", "make_qk_norm_rope",
+    "make_qk_norm_rope_interleaved", "make_rope_cache",
+]
+
+
+def _bf16_only(dtype) -> None:
+    """The reference's `dtype` keyword (ninetoothed.bfloat16 by default): the
+    gfx950 kernels are bf16 kernels."""
+    if dtype is None:
+        return
+    name = str(getattr(dtype, "name", dtype)).lower()
+    if name not in ("bfloat16", "torch.bfloat16", "bf16"):
+        raise ValueError(f"only bfloat16 kernels are built for gfx950, got dtype={dtype!r}")
+
+
+def _bf16(*tensors: torch.Tensor) -> torch.device:
+    device = _lib.check_cuda(*tensors)
+    _lib.check_dtype(torch.bfloat16, *tensors)
+    return device
+
+
+def _ndim(n: int, **tensors: torch.Tensor) -> None:
+    for name, t in tensors.items():
+        if t.dim() != n:
+            raise ValueError(f"{name} must be {n}-D, got shape {tuple(t.shape)}")
+
+
+def make_swiglu(caller="torch", output_dir=None, archs=None, rows=1, cols=1024, num_warps=4, dtype=None):
+    """out = bf16(up * bf16(g / (1 + exp(-g)))) on [B, S, F] (tools/h3_pointwise.py:18-34)."""
+    _bf16_only(dtype)
+
+    def kernel(up, gate, out):
+        _ndim(3, up=up, gate=gate, out=out)
+        device = _bf16(up, gate, out)
+        _lib.launch("launch_h3_swiglu_exact", device, _lib.tensor(up), _lib.tensor(gate), _lib.tensor(out))
+
+    return kernel
+
+
+def make_rms(caller="torch", output_dir=None, archs=None, width=5376, dtype=None):
+    """RMSNorm with bf16 rounding per step on [B, S, width] (tools/h3_pointwise.py:46-70)."""
+    _bf16_only(dtype)
+    if width is not None and width <= 0:
+        raise ValueError("width must be positive")
+    name = {128: "launch_h3_rms_exact_128", 5376: "launch_h3_rms_exact_5376"}.get(width, "launch_h3_rms_exact")
+
+    def kernel(x, weight, eps, out):
+        _ndim(3, x=x, out=out)
+        _ndim(1, weight=weight)
+        if width is not None and x.shape[-1] != width:
+            raise ValueError(f"this kernel was made for width {width}, got {x.shape[-1]}")
+        device = _bf16(x, weight, out)
+        _lib.launch(name, device, _lib.tensor(x), _lib.tensor(weight), _lib.scalar(eps), _lib.tensor(out))
+
+    return kernel
+
+
+def make_rms_modulate(caller="torch", output_dir=None, archs=None, dtype=None):
+    """RMSNorm + AdaLN: bf16(bf16(bf16(rms(x) w) bf16(1 + scale)) + shift)
+    (tools/h3_pointwise.py:83-108), any width."""
+    _bf16_only(dtype)
+
+    def kernel(x, weight, eps, scale, shift, out):
+        _ndim(3, x=x, scale=scale, shift=shift, out=out)
+        _ndim(1, weight=weight)
+        device = _bf16(x, weight, scale, shift, out)
+        _lib.launch("launch_h3_rms_modulate_exact", device, _lib.tensor(x), _lib.tensor(weight),
+                    _lib.scalar(eps), _lib.tensor(scale), _lib.tensor(shift), _lib.tensor(out))
+
+    return kernel
+
+
+def make_gated_residual(caller="torch", output_dir=None, archs=None, block=(4, 512), num_warps=8, dtype=None):
+    """out = bf16(x + bf16(gate * y)) (tools/h3_pointwise.py:121-136)."""
+    _bf16_only(dtype)
+
+    def kernel(x, gate, y, out):
+        _ndim(3, x=x, gate=gate, y=y, out=out)
+        device = _bf16(x, gate, y, out)
+        _lib.launch("launch_h3_gated_residual_exact", device, _lib.tensor(x), _lib.tensor(gate),
+                    _lib.tensor(y), _lib.tensor(out))
+
+    return kernel
+
+
+def make_gated_residual_rms_modulate(caller="torch", output_dir=None, archs=None, num_warps=4, dtype=None):
+    """residual = bf16(x + bf16(gate * y)); out = rms_modulate(residual)
+    (tools/h3_pointwise.py:150-182)."""
+    _bf16_only(dtype)
+
+    def kernel(x, gate, y, weight, eps, scale, shift, residual, out):
+        _ndim(3, x=x, gate=gate, y=y, scale=scale, shift=shift, residual=residual, out=out)
+        _ndim(1, weight=weight)
+        device = _bf16(x, gate, y, weight, scale, shift, residual, out)
+        _lib.launch("launch_h3_gated_residual_rms_modulate_exact", device, _lib.tensor(x), _lib.tensor(gate),
+                    _lib.tensor(y), _lib.tensor(weight), _lib.scalar(eps), _lib.tensor(scale),
+                    _lib.tensor(shift), _lib.tensor(residual), _lib.tensor(out))
+
+    return kernel
+
+
+def make_rope(caller="torch", output_dir=None, archs=None, dtype=None):
+    """Rotate-half RoPE on channels 0..95 of [S, H, 128], cos/sin [S, 48]
+    (tools/h3_pointwise.py:199-231). Returns launch(x, cos, sin, out)."""
+    _bf16_only(dtype)
+
+    def launch(x, cos, sin, out):
+        _ndim(3, x=x, out=out)
+        _ndim(2, cos=cos, sin=sin)
+        device = _bf16(x, cos, sin, out)
+        xa, oa = _lib.tensor(x), _lib.tensor(out)
+        _lib.launch("launch_h3_rope_exact", device, xa, xa, xa, _lib.tensor(cos), _lib.tensor(sin), oa, oa, oa)
+
+    return launch
+
+
+def _qk_raw(x0, x1, xp, w0, w1, wp, eps, cos, sin, y0, y1, yp):
+    _ndim(4, x0=x0, x1=x1, xp=xp, y0=y0, y1=y1, yp=yp)
+    _ndim(1, w0=w0, w1=w1, wp=wp)
+    _ndim(2, cos=cos, sin=sin)
+    device = _bf16(x0, x1, xp, w0, w1, wp, cos, sin, y0, y1, yp)
+    _lib.launch("launch_h3_qk_norm_rope", device, _lib.tensor(x0), _lib.tensor(x1), _lib.tensor(xp),
+                _lib.tensor(w0), _lib.tensor(w1), _lib.tensor(wp), _lib.scalar(eps), _lib.tensor(cos),
+                _lib.tensor(sin), _lib.tensor(y0), _lib.tensor(y1), _lib.tensor(yp))
+
+
+def make_qk_norm_rope(caller="torch", output_dir=None, archs=None, rows=8, num_warps=1, block_tokens=1, ranks=1,
+                      dtype=None):
+    """Per-head RMSNorm (weight [128]) + rotate-half RoPE on x [T, P, Hs, 128]
+    (any strides) into out [T, P, Hs, 128] (any strides), cos/sin [T, 48]
+    (tools/h3_pointwise.py:262-294,370-402). caller="torch" returns
+    launch(x, weight, eps, cos, sin, out); any other caller returns the raw
+    12-argument kernel (x, x, x, w, w, w, eps, cos, sin, out, out, out)."""
+    _bf16_only(dtype)
+    if block_tokens != 1 and ranks != 1:
+        raise ValueError("qk_norm_rope: block_tokens > 1 needs ranks == 1")
+    if caller != "torch":
+        return _qk_raw
+
+    def launch(x, weight, eps, cos, sin, out):
+        _qk_raw(x, x, x, weight, weight, weight, eps, cos, sin, out, out, out)
+
+    return launch
+
+
+def make_qk_norm_rope_interleaved(dtype=None):
+    """Per-head RMSNorm then interleaved-pair RoPE over all 128 channels (pair i =
+    channels 2i, 2i+1; cos/sin [T, 64]); the rounding steps of make_qk_norm_rope.
+    Returns launch(x, weight, eps, cos, sin, out). No counterpart in the
+    reference; it serves the 32/48/48 interleaved RoPE layout."""
+    _bf16_only(dtype)
+
+    def launch(x, weight, eps, cos, sin, out):
+        _ndim(4, x=x, out=out)
+        _ndim(1, weight=weight)
+        _ndim(2, cos=cos, sin=sin)
+        device = _bf16(x, weight, cos, sin, out)
+        _lib.launch("launch_h3_qk_norm_rope_interleaved", device, _lib.tensor(x), _lib.tensor(weight),
+                    _lib.scalar(eps), _lib.tensor(cos), _lib.tensor(sin), _lib.tensor(out))
+
+    return launch
+
+
+def make_rope_cache(caller="torch", output_dir=None, archs=None, block_tokens=64, num_warps=4, dtype=None):
+    """H3's RoPE table: position [T, 3] fp64 and power [16] fp32 to cos/sin
+    [T, 48] bf16 views (tools/h3_pointwise.py:405-442).
+    Returns kernel(position, power, cos, sin)."""
+    _bf16_only(dtype)
+
+    def kernel(position, power, cos, sin):
+        _ndim(2, position=position, cos=cos, sin=sin)
+        _ndim(1, power=power)
+        device = _lib.check_cuda(position, power, cos, sin)
+        _lib.check_dtype(torch.float64, position)
+        _lib.check_dtype(torch.float32, power)
+        _lib.check_dtype(torch.bfloat16, cos, sin)
+        _lib.launch("launch_h3_rope_cache", device, _lib.tensor(position), _lib.tensor(power),
+                    _lib.tensor(cos), _lib.tensor(sin))
+
+    return kernel

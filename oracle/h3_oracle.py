@@ -1,0 +1,357 @@
+"""CPU oracle for the H3 DiT hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker (or, for the CPU baseline, as the thing
+timed on the host). The product path (the package's libh3mi355x.so) never calls
+it and has no CPU fallback.
+
+Each function restates the reference's own torch composition for one op, on
+the CPU, from the cited text:
+  - per-step bf16 rounding of tools/h3_pointwise.py (the NineToothed kernels)
+    and tools/bench_h3_ops.py:81-113,215,232-234,251-254 (the eager baselines
+    those kernels are checked against bitwise);
+  - attention as softmax(q k^T scale) v in fp64 / fp32
+    (tools/verify_attention.py:60-65, tools/tune_attention.py:260-264).
+
+The one free choice the reference leaves open is the order of the fp32 sum of
+squares in the RMS family (Triton's tl.sum tree in the kernels, torch's own
+order in the eager path; the two differ between themselves). `fixed_order_sum`
+states the order the gfx950 kernels use; `order="torch"` selects torch's sum,
+the literal eager composition.
+
+How each function is pinned (tests/test_oracle.py):
+  swiglu                    exhaustive over all 65,536 bf16 gate values against
+                            a float64 closed form; up = 1, 0, -1, powers of two
+  gated_residual            closed forms (gate 0/1/-1, y = x), float64 check of
+                            the rounding chain, special values
+  rms_norm / rms_modulate   constant rows (closed form), zero rows, power-of-two
+  / gated_residual_...      scale invariance (bitwise), fixed-order sum vs fp64
+                            sum bound, float64 reference within 2 bf16 ulp,
+                            scale=-1 and scale=0 modulation, fusion = unfused
+  rope_rotate_half          angle 0 = identity, angle pi/2 = exact rotation with
+                            the i <-> i+48 pairing, pass-through bits, norm
+  qk_norm_rope(_interleaved) = rms_norm(W=128) then the RoPE (composition),
+                            angle cases as above for the (2i, 2i+1) pairing
+  rope_cache                float64 cos/sin within 1 bf16 ulp; closed-form
+                            powers; position 0 row exact
+  attention                 float64 brute force on tiny shapes, torch SDPA,
+                            invariants (key permutation, constant V, identical
+                            keys -> mean V, Sk = 1, dominant key, scale 0)
+  attention_fp8_emulated    fp32 attention within relative RMS 5e-2 (only pin:
+                            the reference has no fp8 path -- parity partial)
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+
+# ----------------------------------------------------------------- rounding
+
+def rb(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> bf16 (round to nearest even) -> fp32: `.to(bfloat16)` of the
+    reference compositions, kept in fp32 for the next step."""
+    return x.to(BF16).to(F32)
+
+
+def fixed_order_sum(sq: torch.Tensor) -> torch.Tensor:
+    """fp32 sum over the last axis in the order of the gfx950 RMS kernels.
+
+    W8 = ceil(W/8) groups of 8 consecutive elements; W8 <= 64: one group per
+    lane, L = next power of two >= W8 lanes; else 256 threads, thread t owning
+    groups t, t+256, ...; each thread adds its elements left to right into one
+    fp32 partial starting at +0; partials fold pairwise within each 64-lane wave
+    (p[:n] + p[n:2n], n = L/2 ... 1), then across the 4 waves as
+    (w0 + w2) + (w1 + w3)."""
+    sq = sq.to(F32)
+    W = sq.shape[-1]
+    groups = -(-W // 8)
+    if groups <= 64:
+        threads = 1
+        while threads < groups:
+            threads *= 2
+    else:
+        threads = 256
+    J = -(-groups // threads)
+    lead = sq.shape[:-1]
+    padded = torch.zeros(*lead, J * threads * 8, dtype=F32)
+    padded[..., :W] = sq
+    v = padded.view(*lead, J, threads, 8)
+    partial = torch.zeros(*lead, threads, dtype=F32)
+    for j in range(J):
+        for e in range(8):
+            partial = partial + v[..., j, :, e]
+    lanes = min(threads, 64)
+    p = partial.view(*lead, threads // lanes, lanes)
+    n = lanes
+    while n > 1:
+        n //= 2
+        p = p[..., :n] + p[..., n:2 * n]
+    p = p[..., 0]
+    n = threads // lanes
+    while n > 1:
+        n //= 2
+        p = p[..., :n] + p[..., n:2 * n]
+    return p[..., 0]
+
+
+def _eps(eps: float, eps_rounding: str) -> torch.Tensor:
+    e = torch.tensor(eps, dtype=F32)
+    if eps_rounding == "bf16":
+        return rb(e)  # tools/h3_pointwise.py:52-53 (fp64 -> fp32 -> bf16)
+    if eps_rounding == "fp32":
+        return e  # tools/bench_h3_ops.py:86
+    raise ValueError(eps_rounding)
+
+
+# ----------------------------------------------------------------- pointwise
+
+def rms_reciprocal(value: torch.Tensor, eps: float, order: str = "fixed", eps_rounding: str = "bf16") -> torch.Tensor:
+    """bf16 reciprocal RMS of fp32 `value` rows (already bf16 values):
+    tools/h3_pointwise.py:49-55, tools/bench_h3_ops.py:84-87."""
+    W = value.shape[-1]
+    squared = rb(value * value)
+    total = fixed_order_sum(squared) if order == "fixed" else squared.sum(-1)
+    mean = rb(total / W)
+    variance = rb(mean + _eps(eps, eps_rounding))
+    # rsqrt as 1/sqrt with two IEEE roundings (what torch's CPU rsqrt computes).
+    return rb(1.0 / torch.sqrt(variance)).unsqueeze(-1)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, order: str = "fixed",
+             eps_rounding: str = "bf16") -> torch.Tensor:
+    """tools/h3_pointwise.py:46-57 / tools/bench_h3_ops.py:81-88."""
+    value = x.float()
+    r = rms_reciprocal(value, eps, order, eps_rounding)
+    normalized = rb(value * r)
+    return (normalized * weight.float()).to(BF16)
+
+
+def modulate(normalized: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
+    """tools/bench_h3_ops.py:91-93 (tools/h3_pointwise.py:95-97)."""
+    factor = rb(scale.float() + 1.0)
+    product = rb(normalized.float() * factor)
+    return (product + shift.float()).to(BF16)
+
+
+def rms_modulate(x, weight, eps, scale, shift, order="fixed", eps_rounding="bf16"):
+    """tools/h3_pointwise.py:83-97."""
+    return modulate(rms_norm(x, weight, eps, order, eps_rounding), scale, shift)
+
+
+def gated_residual(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """out = bf16(x + bf16(gate * y)): tools/h3_pointwise.py:121-124,
+    tools/bench_h3_ops.py:215 (torch.add(x, torch.mul(gate, y)) in bf16)."""
+    product = rb(gate.float() * y.float())
+    return (x.float() + product).to(BF16)
+
+
+def gated_residual_rms_modulate(x, gate, y, weight, eps, scale, shift, order="fixed", eps_rounding="bf16"):
+    """tools/h3_pointwise.py:150-168, tools/bench_h3_ops.py:232-234.
+    Returns (residual, out)."""
+    residual = gated_residual(x, gate, y)
+    return residual, rms_modulate(residual, weight, eps, scale, shift, order, eps_rounding)
+
+
+def swiglu(up: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """tools/h3_pointwise.py:18-22, tools/bench_h3_ops.py:251-254."""
+    value = gate.float()
+    activated = rb(value / (1.0 + torch.exp(-value)))
+    return (up.float() * activated).to(BF16)
+
+
+def rope_rotate_half(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """3-axis NeoX RoPE on channels 0..95 (pairs i, i+48), 96..127 pass through:
+    tools/h3_pointwise.py:199-214, tools/bench_h3_ops.py:96-106. cos/sin must
+    broadcast against x[..., :48]."""
+    a, b, passthrough = x[..., :48].float(), x[..., 48:96].float(), x[..., 96:]
+    c, s = cos.float(), sin.float()
+    ac, bs = rb(a * c), rb(-b * s)
+    bc, a_s = rb(b * c), rb(a * s)
+    return torch.cat([(ac + bs).to(BF16), (bc + a_s).to(BF16), passthrough.to(BF16)], dim=-1)
+
+
+def rope_interleaved(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Interleaved-pair RoPE over 128 channels: pair i = (2i, 2i+1), with the
+    same four bf16-rounded products as the rotate-half form. cos/sin [..., 64]."""
+    a, b = x[..., 0::2].float(), x[..., 1::2].float()
+    c, s = cos.float(), sin.float()
+    ac, bs = rb(a * c), rb(-b * s)
+    bc, a_s = rb(b * c), rb(a * s)
+    out = torch.stack([(ac + bs), (bc + a_s)], dim=-1).flatten(-2)
+    return out.to(BF16)
+
+
+def qk_norm_rope(x, weight, eps, cos, sin, order="fixed", eps_rounding="bf16"):
+    """Per-head RMSNorm (W = 128) then rotate-half RoPE on x [T, P, Hs, 128],
+    cos/sin [T, 48]: tools/h3_pointwise.py:262-294, tools/bench_h3_ops.py:145-149."""
+    normalized = rms_norm(x, weight, eps, order, eps_rounding)
+    return rope_rotate_half(normalized, cos[:, None, None, :], sin[:, None, None, :])
+
+
+def qk_norm_rope_interleaved(x, weight, eps, cos, sin, order="fixed", eps_rounding="bf16"):
+    """Per-head RMSNorm (W = 128) then interleaved-pair RoPE, cos/sin [T, 64]."""
+    normalized = rms_norm(x, weight, eps, order, eps_rounding)
+    return rope_interleaved(normalized, cos[:, None, None, :], sin[:, None, None, :])
+
+
+def rope_powers(rope_freq_dim: int = 16, rope_theta: float = 10000.0) -> torch.Tensor:
+    """power[k] = theta ** (2k / 32) in fp32 (patches/InfiniLM.patch:7013-7021,
+    tools/bench_h3_ops.py:172-173)."""
+    exponent = torch.tensor([2 * k / (2 * rope_freq_dim) for k in range(rope_freq_dim)], dtype=F32)
+    return torch.full_like(exponent, rope_theta) ** exponent
+
+
+def rope_cache(position: torch.Tensor, power: torch.Tensor) -> torch.Tensor:
+    """[T, 96] bf16 = cat(cos, sin)(fp32(position[T, a]) * (1 / power[k])):
+    tools/h3_pointwise.py:416-427, patches/InfiniLM.patch:6605-6635."""
+    inverse = 1.0 / power.to(F32)
+    frequencies = (position.to(F32).unsqueeze(-1) * inverse.view(1, 1, -1)).flatten(1)
+    return torch.cat((frequencies.cos(), frequencies.sin()), dim=-1).to(BF16)
+
+
+def grid_positions(t: int, h: int, w: int) -> torch.Tensor:
+    """(t, h, w) token grid, row-major with t slowest, as fp64 [T, 3]."""
+    tt, hh, ww = torch.meshgrid(torch.arange(t), torch.arange(h), torch.arange(w), indexing="ij")
+    return torch.stack([tt.flatten(), hh.flatten(), ww.flatten()], dim=-1).to(torch.float64)
+
+
+def rope_table_interleaved(position: torch.Tensor, axes=(32, 48, 48), theta: float = 10000.0):
+    """cos/sin [T, 64] bf16 for the interleaved 32/48/48 layout: pair j of axis
+    a (dim d_a) rotates by position[:, a] * theta ** (-2j / d_a), in fp32."""
+    freqs = []
+    for a, d in enumerate(axes):
+        j = torch.arange(d // 2, dtype=F32)
+        inv = 1.0 / (torch.tensor(theta, dtype=F32) ** (2.0 * j / d))
+        freqs.append(position[:, a].to(F32).unsqueeze(-1) * inv)
+    angle = torch.cat(freqs, dim=-1)
+    return angle.cos().to(BF16), angle.sin().to(BF16)
+
+
+# ----------------------------------------------------------------- attention
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, dtype=torch.float64,
+              chunk: int = 1024) -> torch.Tensor:
+    """softmax(q k^T scale) v on [B, H, S, D] in `dtype` (fp64 or fp32),
+    chunked over queries (tools/verify_attention.py:63-64)."""
+    B, H, Sq, D = q.shape
+    out = torch.empty(B, H, Sq, v.shape[-1], dtype=dtype)
+    kt = k.to(dtype).transpose(-2, -1).contiguous()
+    vd = v.to(dtype).contiguous()
+    for s0 in range(0, Sq, chunk):
+        logits = torch.matmul(q[:, :, s0:s0 + chunk].to(dtype), kt) * scale
+        out[:, :, s0:s0 + chunk] = torch.matmul(torch.softmax(logits, dim=-1), vd)
+    return out
+
+
+def attention_rows(q, k, v, scale, rows: torch.Tensor, dtype=torch.float64) -> torch.Tensor:
+    """The attention of selected query rows (the sampled-row check of
+    tools/verify_attention.py:62-65)."""
+    return attention(q[:, :, rows], k, v, scale, dtype=dtype)
+
+
+E4M3_MAX = 448.0
+
+
+def quantize_fp8_per_head(x: torch.Tensor):
+    """Per-head absmax e4m3fn quantisation of [B, H, S, D]: descale[h] =
+    amax_h / 448; codes = e4m3fn(x * (448 / amax_h)). Returns (codes as
+    torch.float8_e4m3fn, descale fp32 [H])."""
+    xf = x.float()
+    amax = xf.abs().amax(dim=(0, 2, 3))
+    inv = torch.where(amax > 0, E4M3_MAX / amax, torch.zeros_like(amax))
+    codes = (xf * inv.view(1, -1, 1, 1)).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    descale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+    return codes, descale
+
+
+def attention_fp8_emulated(q8, k8, v8, q_descale, k_descale, v_descale, scale: float, block_n: int = 64):
+    """The fp8 algorithm on the CPU: fp32 logits from e4m3 codes times
+    q_descale*k_descale*scale, exp2 online softmax over `block_n`-key tiles, P
+    requantised per tile to e4m3 with the fixed factor 448, fp32 P.V, output
+    acc * v_descale / (448 * denominator) in bf16. [B, H, S, D]."""
+    B, H, Sq, D = q8.shape
+    Sk = k8.shape[2]
+    qf, kf, vf = q8.float(), k8.float(), v8.float()
+    c = (q_descale * k_descale).view(1, H, 1, 1) * (scale * 1.4426950408889634)
+    m = torch.full((B, H, Sq, 1), -math.inf)
+    den = torch.zeros(B, H, Sq, 1)
+    acc = torch.zeros(B, H, Sq, D)
+    for k0 in range(0, Sk, block_n):
+        logits = torch.matmul(qf, kf[:, :, k0:k0 + block_n].transpose(-2, -1)) * c
+        m_new = torch.maximum(m, logits.amax(-1, keepdim=True))
+        p = torch.exp2(logits - m_new)
+        alpha = torch.exp2(m - m_new)
+        p8 = (p * E4M3_MAX).to(torch.float8_e4m3fn).float()
+        acc = acc * alpha + torch.matmul(p8, vf[:, :, k0:k0 + block_n])
+        den = den * alpha + p.sum(-1, keepdim=True)
+        m = m_new
+    return (acc * v_descale.view(1, H, 1, 1) / (E4M3_MAX * den)).to(BF16)
+
+
+# ----------------------------------------------------------------- inputs
+
+def _randn(gen, *shape):
+    return torch.randn(*shape, generator=gen, dtype=F32)
+
+
+def attention_inputs(S: int, H: int = 14, D: int = 128, seed: int = 0, outlier_fraction: float = 0.0,
+                     outlier_scale: float = 8.0):
+    """q, k, v [1, S, H, D] bf16 ~ N(0, 1), drawn q, k, v from a CPU generator
+    seeded `seed`; optionally `outlier_fraction` of the key rows (all heads)
+    scaled by `outlier_scale` (exact in bf16 for a power of two)."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    q, k, v = (_randn(gen, 1, S, H, D).to(BF16) for _ in range(3))
+    if outlier_fraction > 0:
+        rows = torch.randperm(S, generator=gen)[: int(round(S * outlier_fraction))]
+        k[:, rows] = (k[:, rows].float() * outlier_scale).to(BF16)
+    return q, k, v
+
+
+def qk_norm_rope_inputs(T: int = 8192, H: int = 14, seed: int = 0, grid=(8, 32, 32)):
+    """q, k [1, T, H, 128] bf16 ~ N(0, 1); w_q, w_k = 1 + 0.1 N(0, 1) [128];
+    positions from the (t, h, w) grid (truncated / tiled to T)."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    q = _randn(gen, 1, T, H, 128).to(BF16)
+    k = _randn(gen, 1, T, H, 128).to(BF16)
+    w_q = (1.0 + 0.1 * _randn(gen, 128)).to(BF16)
+    w_k = (1.0 + 0.1 * _randn(gen, 128)).to(BF16)
+    pos = grid_positions(*grid)
+    if pos.shape[0] < T:
+        pos = pos.repeat(-(-T // pos.shape[0]), 1)
+    return q, k, w_q, w_k, pos[:T].contiguous()
+
+
+def chain_inputs(S: int = 8192, C: int = 7168, F: int = 18432, seed: int = 0):
+    """The AdaLN / SwiGLU / gated-residual chain inputs, drawn in the order x,
+    shift, scale, gate, up, gate_act, residual, y, w."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    x = _randn(gen, S, C).to(BF16)
+    shift = (0.1 * _randn(gen, 1, C)).to(BF16)
+    scale = (0.1 * _randn(gen, 1, C)).to(BF16)
+    gate = (0.1 * _randn(gen, 1, C)).to(BF16)
+    up = _randn(gen, S, F).to(BF16)
+    gate_act = _randn(gen, S, F).to(BF16)
+    residual = _randn(gen, S, C).to(BF16)
+    y = _randn(gen, S, C).to(BF16)
+    w = (1.0 + 0.1 * _randn(gen, C)).to(BF16)
+    return dict(x=x, shift=shift, scale=scale, gate=gate, up=up, gate_act=gate_act, residual=residual, y=y, w=w)
+
+
+# ----------------------------------------------------------------- metrics
+
+def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Elementwise distance in bf16 ulps between two bf16 tensors (NaN == NaN
+    counts as 0; +0 and -0 are 0 apart)."""
+    ia = a.to(BF16).view(torch.int16).to(torch.int32)
+    ib = b.to(BF16).view(torch.int16).to(torch.int32)
+    # Map sign-magnitude to a monotone integer line.
+    ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)
+    ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    d = (ia - ib).abs()
+    both_nan = torch.isnan(a.float()) & torch.isnan(b.float())
+    return torch.where(both_nan, torch.zeros_like(d), d)

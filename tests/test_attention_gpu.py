@@ -1,0 +1,118 @@
+"""GPU parity of the bf16 attention kernel.
+
+Bar (north star): max |err| <= 2e-2 and relative RMS <= 1e-2 against an fp32
+(or fp64) softmax(q k^T s) v reference. Small and ragged shapes are checked
+against the fp64 CPU oracle; the S = 8192 and S = 73,984 configurations
+against a chunked fp32 reference computed on the GPU with torch (fp32 matmul)
+plus fp64 oracle rows sampled as in tools/verify_attention.py:62-65.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import attention_error
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+MAX_ABS, REL_RMS = 2e-2, 1e-2
+
+
+def _bhsd(x):
+    """[B, S, H, D] -> the kernel's [B, H, S, D] view (strides swapped, as the
+    reference's MHA operator passes it, patches/InfiniCore.patch:1403-1411)."""
+    return x.transpose(1, 2)
+
+
+def gpu_reference_fp32(q, k, v, scale, chunk=512):
+    """softmax(q k^T scale) v in fp32 on the GPU, chunked over queries."""
+    B, H, Sq, D = q.shape
+    out = torch.empty(B, H, Sq, D, dtype=torch.float32, device=q.device)
+    kt = k.float().transpose(-2, -1).contiguous()
+    vf = v.float().contiguous()
+    for s0 in range(0, Sq, chunk):
+        logits = torch.matmul(q[:, :, s0:s0 + chunk].float().contiguous(), kt) * scale
+        out[:, :, s0:s0 + chunk] = torch.matmul(torch.softmax(logits, dim=-1), vf)
+    return out
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk", [
+    (1, 1, 1, 1), (1, 2, 64, 64), (2, 3, 65, 63), (1, 2, 200, 129), (1, 1, 300, 1000),
+    (2, 2, 257, 257), (1, 1, 513, 64),
+])
+def test_attention_small_vs_fp64(pkg, oracle, device, B, H, Sq, Sk):
+    gen = torch.Generator("cpu").manual_seed(Sq * 7 + Sk)
+    q = torch.randn(B, Sq, H, 128, generator=gen).to(BF)
+    k = torch.randn(B, Sk, H, 128, generator=gen).to(BF)
+    v = torch.randn(B, Sk, H, 128, generator=gen).to(BF)
+    scale = 128 ** -0.5
+    qd, kd, vd = (t.to(device) for t in (q, k, v))
+    out = torch.empty(B, Sq, H, 128, dtype=BF, device=device)
+    pkg.make_attention()(_bhsd(qd), _bhsd(kd), _bhsd(vd), scale, _bhsd(out))
+    torch.cuda.synchronize()
+    ref = oracle.attention(_bhsd(q), _bhsd(k), _bhsd(v), scale)
+    mx, rel = attention_error(_bhsd(out).cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
+def test_attention_packed_qkv(pkg, oracle, device):
+    """q, k, v as strided slices of one packed [1, S, 3, H, D] tensor
+    (tools/verify_attention.py:42-43)."""
+    gen = torch.Generator("cpu").manual_seed(2026)
+    S, H = 1024, 14
+    packed = torch.randn(1, S, 3, H, 128, generator=gen).to(BF)
+    pd = packed.to(device)
+    q, k, v = (pd[:, :, i].transpose(1, 2) for i in range(3))
+    out = torch.empty(1, H, S, 128, dtype=BF, device=device)
+    pkg.make_attention()(q, k, v, 128 ** -0.5, out)
+    torch.cuda.synchronize()
+    ref = oracle.attention(*(packed[:, :, i].transpose(1, 2) for i in range(3)), 128 ** -0.5)
+    mx, rel = attention_error(out.cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+    # Repeat determinism (tools/verify_attention.py:54-59).
+    first = out.clone()
+    pkg.make_attention()(q, k, v, 128 ** -0.5, out)
+    torch.cuda.synchronize()
+    assert torch.equal(first, out)
+
+
+def test_attention_scale_edge_cases(pkg, oracle, device):
+    gen = torch.Generator("cpu").manual_seed(5)
+    q = torch.randn(1, 2, 130, 128, generator=gen).to(BF)
+    k = torch.randn(1, 2, 190, 128, generator=gen).to(BF)
+    v = torch.randn(1, 2, 190, 128, generator=gen).to(BF)
+    for scale in (0.0, -0.05, 0.5):
+        out = torch.empty_like(q, device=device)
+        pkg.make_attention()(q.to(device), k.to(device), v.to(device), scale, out)
+        torch.cuda.synchronize()
+        ref = oracle.attention(q, k, v, scale)
+        mx, rel = attention_error(out.cpu(), ref)
+        assert mx <= MAX_ABS and rel <= REL_RMS, (scale, mx, rel)
+
+
+def _config_check(pkg, oracle, device, S, outlier_fraction):
+    q, k, v = oracle.attention_inputs(S, outlier_fraction=outlier_fraction)
+    scale = 128 ** -0.5
+    qd, kd, vd = (t.to(device) for t in (q, k, v))
+    out = torch.empty_like(qd)
+    pkg.make_attention()(_bhsd(qd), _bhsd(kd), _bhsd(vd), scale, _bhsd(out))
+    torch.cuda.synchronize()
+    ref = gpu_reference_fp32(_bhsd(qd), _bhsd(kd), _bhsd(vd), scale)
+    mx, rel = attention_error(_bhsd(out), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+    rows = torch.linspace(0, S - 1, 16).long()
+    ref_rows = oracle.attention_rows(_bhsd(q), _bhsd(k), _bhsd(v), scale, rows)
+    mx, rel = attention_error(_bhsd(out)[:, :, rows].cpu(), ref_rows)
+    assert mx <= MAX_ABS and rel <= REL_RMS, ("fp64 rows", mx, rel)
+    return out
+
+
+def test_attention_config_s8192(pkg, oracle, device):
+    _config_check(pkg, oracle, device, 8192, 0.0)
+
+
+def test_attention_config_s73984_peaky(pkg, oracle, device):
+    """S = 73,984 (32x48x48 video + 256 text tokens), H = 14, 1% of key rows x8."""
+    _config_check(pkg, oracle, device, 73984, 0.01)
