@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark of the H3 DiT hot path on one MI355X.
+
+Headline (one JSON line on stdout): non-causal bf16 attention forward at
+S = 73,984 (32x48x48 video latents + 256 text tokens), H = 14, D = 128, B = 1,
+q/k/v ~ N(0, 1) with 1% of key rows x8, in the [B, S, H, D] layout the
+reference's MHA operator receives. One step = one attention forward over the
+whole sequence; value = 4*B*H*S^2*D flops / seconds per step (the reference's
+formula, tools/bench_h3_ops.py:125).
+
+Extra fields on the same line:
+  roofline      the attention kernel against the bf16 dense MFMA peak
+  cpu_baseline  the CPU oracle's fp32 attention on a bounded sample of the same
+                workload, on this host's cores
+  pointwise     GB/s of each fused pointwise op at its configuration size
+                (q/k [1, 8192, 14, 128]; [8192, 7168] / [8192, 18432]), timed
+                as back-to-back launches in a HIP graph over rotating buffers
+                larger than the 256 MB last-level cache
+  attention_s8192, fp8   further attention configurations
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+METRIC = "attn TFLOP/s (% MFMA peak) at S=73,984 H=14 D=128; fused-op HBM GB/s"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def attention_inputs_gpu(S: int, H: int, seed: int, outlier_fraction: float, device):
+    """q, k, v [1, S, H, 128] bf16 ~ N(0, 1) from a seeded device generator;
+    `outlier_fraction` of key rows scaled x8 (exact in bf16)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q, k, v = (torch.randn(1, S, H, 128, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+               for _ in range(3))
+    if outlier_fraction > 0:
+        rows = torch.randperm(S, generator=gen, device=device)[: int(round(S * outlier_fraction))]
+        k[:, rows] *= 8
+    return q, k, v
+
+
+def time_launches(fn, steps: int, warmup: int) -> float:
+    """Mean milliseconds per call: `warmup` untimed calls, then `steps` calls
+    bracketed by synchronize + HIP events on the launch stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_graph(calls, repeats: int = 20) -> float:
+    """Mean milliseconds per launch of `calls` (a list of zero-argument
+    launches) captured back to back in one HIP graph, replayed `repeats` times."""
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(repeats):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (repeats * len(calls))
+
+
+def bench_pointwise(pkg, device) -> dict:
+    """GB/s per op; bytes = compulsory bf16 reads + writes (broadcast vectors
+    counted once)."""
+    results = {}
+    gen = torch.Generator(device=device).manual_seed(0)
+    bf = torch.bfloat16
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=gen, device=device) * scale).to(bf)
+
+    def record(name, ms, nbytes, shape):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        results[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes": nbytes, "shape": shape}
+        log(f"  {name:34s} {ms * 1e3:8.2f} us  {gbs:8.1f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+
+    # q/k RMSNorm + RoPE, [1, 8192, 14, 128] per tensor, both layouts.
+    T, H = 8192, 14
+    rot = 12  # 12 x 2 x 29 MB > 512 MB
+    xs = [rnd(T, 1, H, 128) for _ in range(rot)]
+    outs = [torch.empty_like(x) for x in xs]
+    w = rnd(128, scale=0.1) + 1
+    table64 = rnd(T, 128)
+    table48 = rnd(T, 96)
+    k_int = pkg.make_qk_norm_rope_interleaved()
+    k_rh = pkg.make_qk_norm_rope()
+    nbytes = 2 * T * H * 128 * 2 + T * 64 * 2 * 2 + 128 * 2
+    ms = time_graph([lambda x=x, o=o: k_int(x, w, 1e-6, table64[:, :64], table64[:, 64:], o) for x, o in zip(xs, outs)])
+    record("qk_norm_rope_interleaved", ms, nbytes, [T, 1, H, 128])
+    nbytes = 2 * T * H * 128 * 2 + T * 48 * 2 * 2 + 128 * 2
+    ms = time_graph([lambda x=x, o=o: k_rh(x, w, 1e-6, table48[:, :48], table48[:, 48:], o) for x, o in zip(xs, outs)])
+    record("qk_norm_rope", ms, nbytes, [T, 1, H, 128])
+    del xs, outs
+
+    S, C, F = 8192, 7168, 18432
+    rot = 3
+    xs = [rnd(1, S, C) for _ in range(rot)]
+    ys = [rnd(1, S, C) for _ in range(rot)]
+    outs = [torch.empty_like(x) for x in xs]
+    res = [torch.empty_like(x) for x in xs]
+    wC = rnd(C, scale=0.1) + 1
+    scale = rnd(1, 1, C, scale=0.1).expand(1, S, C)
+    shift = rnd(1, 1, C, scale=0.1).expand(1, S, C)
+    gate = rnd(1, 1, C, scale=0.1).expand(1, S, C)
+    k_mod = pkg.make_rms_modulate()
+    ms = time_graph([lambda x=x, o=o: k_mod(x, wC, 1e-6, scale, shift, o) for x, o in zip(xs, outs)])
+    record("rms_modulate", ms, 2 * S * C * 2 + 3 * C * 2, [1, S, C])
+    k_gr = pkg.make_gated_residual()
+    ms = time_graph([lambda x=x, y=y, o=o: k_gr(x, gate, y, o) for x, y, o in zip(xs, ys, outs)])
+    record("gated_residual", ms, 3 * S * C * 2 + C * 2, [1, S, C])
+    k_grm = pkg.make_gated_residual_rms_modulate()
+    ms = time_graph([lambda x=x, y=y, o=o, r=r: k_grm(x, gate, y, wC, 1e-6, scale, shift, r, o)
+                     for x, y, o, r in zip(xs, ys, outs, res)])
+    record("gated_residual_rms_modulate", ms, 4 * S * C * 2 + 4 * C * 2, [1, S, C])
+    del xs, ys, outs, res
+    ups = [rnd(1, S, F) for _ in range(2)]
+    gates = [rnd(1, S, F) for _ in range(2)]
+    outs = [torch.empty_like(u) for u in ups]
+    k_sw = pkg.make_swiglu()
+    ms = time_graph([lambda u=u, g=g, o=o: k_sw(u, g, o) for u, g, o in zip(ups, gates, outs)])
+    record("swiglu", ms, 3 * S * F * 2, [1, S, F])
+    return results
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """The CPU oracle's fp32 attention (softmax(q k^T s) v, chunked 2048 query
+    rows) on heads of the S = 73,984, H = 14 workload, head after head until
+    `budget_s` seconds have elapsed (at least one head)."""
+    from oracle import h3_oracle
+    S, H = 73984, 14
+    gen = torch.Generator("cpu").manual_seed(0)
+    threads = torch.get_num_threads()
+    flops = 0.0
+    heads = 0
+    elapsed = 0.0
+    while heads < H and elapsed < budget_s:
+        q, k, v = (torch.randn(1, 1, S, 128, generator=gen).to(torch.bfloat16) for _ in range(3))
+        t_head = time.perf_counter()
+        h3_oracle.attention(q, k, v, 128 ** -0.5, dtype=torch.float32, chunk=2048)
+        elapsed += time.perf_counter() - t_head
+        flops += 4.0 * S * S * 128
+        heads += 1
+    return {"value": round(flops / elapsed / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{heads} of 14 heads of the S=73,984 D=128 attention, fp32 on the host CPU "
+                      f"(oracle softmax(q k^T s) v, 2048-query chunks), {elapsed:.1f} s"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-pointwise", action="store_true")
+    parser.add_argument("--no-extra", action="store_true", help="skip the S=8192 and fp8 attention lines")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU's share (14 heads at full sequence length); runs on more than one "
+              "GPU are not part of this build", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    pkg = importlib.import_module("minimaxh3_on_k100-ai_amd")
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    props = torch.cuda.get_device_properties(device)
+    log(f"device {props.name} ({props.gcnArchName}), torch {torch.__version__}")
+
+    S, H, D = 73984, 14, 128
+    q, k, v = attention_inputs_gpu(S, H, 0, 0.01, device)
+    out = torch.empty_like(q)
+    attn = pkg.make_attention()
+    scale = D ** -0.5
+
+    def step():
+        attn(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale, out.transpose(1, 2))
+
+    ms = time_launches(step, args.steps, args.warmup)
+    flops = 4.0 * S * S * D * H
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"attention S={S} H={H}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS:.1%} of bf16 peak)")
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1), 1% key rows x8)",
+        "config": {"workload": "non-causal bf16 attention forward, B=1 H=14 S=73984 D=128 "
+                               "(73,728 video + 256 text tokens), [B,S,H,D] layout, scale 1/sqrt(128)",
+                   "global_batch": 1, "seq_len": S, "heads": H, "head_dim": D, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    profile = ROOT / "profiles" / "attention_s73984_traffic.json"
+    if profile.exists():
+        line["roofline"]["traffic"] = json.loads(profile.read_text()).get("hbm_bytes_per_launch")
+    del q, k, v, out
+
+    if not args.no_extra:
+        S2 = 8192
+        q, k, v = attention_inputs_gpu(S2, H, 0, 0.0, device)
+        out = torch.empty_like(q)
+        ms2 = time_launches(lambda: attn(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale,
+                                         out.transpose(1, 2)), 20, 3)
+        t2 = 4.0 * S2 * S2 * D * H / (ms2 * 1e-3) / 1e12
+        line["attention_s8192"] = {"ms": round(ms2, 4), "TFLOP/s": round(t2, 2),
+                                   "frac": round(t2 / BF16_PEAK_TFLOPS, 4)}
+        log(f"attention S={S2} H={H}: {ms2:.3f} ms, {t2:.1f} TFLOP/s")
+        del q, k, v, out
+
+    if not args.no_pointwise:
+        log("pointwise ops:")
+        line["pointwise"] = bench_pointwise(pkg, device)
+
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle fp32 attention on the host)...")
+        line["cpu_baseline"] = cpu_baseline()
+        log(f"  {line['cpu_baseline']}")
+
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

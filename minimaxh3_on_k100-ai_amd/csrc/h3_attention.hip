@@ -84,6 +84,113 @@ __device__ __forceinline__ void store_tile(bf16_t *lds, const uint4 reg[4]) {
     for (int r = 0; r < 4; ++r) *reinterpret_cast<uint4 *>(lds + (t / 16 + 16 * r) * kRow + (t % 16) * 8) = reg[r];
 }
 
+// One 64-key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK marks the
+// last, partial tile (keys >= valid are excluded).
+template <bool MASK, bool NEG>
+__device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[2][8],
+                                            f32x16_t (&acc)[4][2], float (&m_run)[2], float (&l_run)[2], float c,
+                                            int krow, int half, int v_row_off, int v_col_off) {
+    f32x16_t s[2][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[ks][qs][i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            const bf16x8_t kop =
+                as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRow + 16 * kk + 8 * half));
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+                s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
+        }
+    }
+
+    bf16x8_t pop[2][4];  // P^T operands: query block x 16-key step
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        if constexpr (MASK) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = 32 * ks + 16 * (i / 8) + 8 * half + (i % 8);
+                    if (key >= valid) s[ks][qs][i] = NEG ? INFINITY : -INFINITY;
+                }
+        }
+        float mx = s[0][qs][0];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][qs][i]) : fmaxf(mx, s[ks][qs][i]);
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
+            mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
+        }
+        const float m_tile = mx * c;  // this tile's row maximum in logit units
+        // Exact running max as in the reference; the accumulators are only
+        // touched when some row's max grew (alpha == 1 exactly otherwise).
+        const bool grow = m_tile > m_run[qs];
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float m_new = grow ? m_tile : m_run[qs];
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_new);
+            m_run[qs] = m_new;
+            l_run[qs] *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[db][qs][i] *= alpha;
+        }
+        const float m_use = m_run[qs];
+        float rowsum = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][qs][i], c, -m_use));
+                if constexpr (MASK) {
+                    const int key = 32 * ks + 16 * (i / 8) + 8 * half + (i % 8);
+                    if (key >= valid) p = 0.0f;
+                }
+                s[ks][qs][i] = p;
+                rowsum += p;
+            }
+        }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
+            rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        l_run[qs] += rowsum;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int ks = t >> 1, base = 8 * (t & 1);
+            uint4 packed;
+            packed.x = pack2(s[ks][qs][base + 0], s[ks][qs][base + 1]);
+            packed.y = pack2(s[ks][qs][base + 2], s[ks][qs][base + 3]);
+            packed.z = pack2(s[ks][qs][base + 4], s[ks][qs][base + 5]);
+            packed.w = pack2(s[ks][qs][base + 6], s[ks][qs][base + 7]);
+            pop[qs][t] = as_bf16x8(packed);
+        }
+    }
+
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const bf16_t *vp = vt + (16 * t + v_row_off) * kRow + 32 * db + v_col_off;
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRow));
+            const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
+            const bf16x8_t vop = as_bf16x8(make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+                acc[db][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop[qs][t], acc[db][qs], 0, 0, 0);
+        }
+    }
+}
+
 template <bool NEG>
 __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_fwd_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElems];
@@ -128,7 +235,6 @@ __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     float m_run[2] = {-INFINITY, -INFINITY};  // running max of the logits
     float l_run[2] = {0.0f, 0.0f};            // running denominator
 
-    const int ntiles = (a.Sk + kBN - 1) / kBN;
     uint4 kreg[4], vreg[4];
     load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
     load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
@@ -144,123 +250,29 @@ __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int v_row_off = 8 * (g16 >> 1) + (s16 >> 2);
     const int v_col_off = 16 * (g16 & 1) + 4 * (s16 & 3);
 
-    for (int tile = 0; tile < ntiles; ++tile) {
+    // Full tiles in the loop; a partial last tile (Sk % 64 != 0) after it.
+    const int full = a.Sk / kBN;
+    for (int tile = 0; tile < full; ++tile) {
         const int buf = tile & 1;
-        const int key0 = tile * kBN;
-        const bool has_next = tile + 1 < ntiles;
+        const int next0 = (tile + 1) * kBN;
+        const bool has_next = next0 < a.Sk;
         if (has_next) {
-            const int nvalid = a.Sk - key0 - kBN < kBN ? a.Sk - key0 - kBN : kBN;
-            load_tile(kbase, a.ks[2], key0 + kBN, nvalid, kreg);
-            load_tile(vbase, a.vs[2], key0 + kBN, nvalid, vreg);
+            const int nvalid = a.Sk - next0 < kBN ? a.Sk - next0 : kBN;
+            load_tile(kbase, a.ks[2], next0, nvalid, kreg);
+            load_tile(vbase, a.vs[2], next0, nvalid, vreg);
         }
-        const bf16_t *kt = lds_k[buf];
-        const bf16_t *vt = lds_v[buf];
-
-        // ---- S^T = K Q^T for 2 key blocks x 2 query blocks
-        f32x16_t s[2][2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s[ks][qs][i] = 0.0f;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const bf16x8_t kop =
-                    as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRow + 16 * kk + 8 * half));
-#pragma unroll
-                for (int qs = 0; qs < 2; ++qs)
-                    s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
-            }
-        }
-
-        // ---- online softmax, per lane (= per query), per query block
-        const int valid = a.Sk - key0;  // keys of this tile that exist (>= 1)
-        bf16x8_t pop[2][4];             // P^T operands: query block x 16-key step
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-            if (valid < kBN) {
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key = 32 * ks + 16 * (i / 8) + 8 * half + (i % 8);
-                        if (key >= valid) s[ks][qs][i] = NEG ? INFINITY : -INFINITY;
-                    }
-            }
-            float mx = s[0][qs][0];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][qs][i]) : fmaxf(mx, s[ks][qs][i]);
-            {
-                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-                const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
-                mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
-            }
-            const float m_new = fmaxf(m_run[qs], mx * a.c);  // running max in logit units
-            const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_new);
-            m_run[qs] = m_new;
-            float rowsum = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][qs][i], a.c, -m_new));
-                    if (valid < kBN) {
-                        const int key = 32 * ks + 16 * (i / 8) + 8 * half + (i % 8);
-                        if (key >= valid) p = 0.0f;
-                    }
-                    s[ks][qs][i] = p;
-                    rowsum += p;
-                }
-            }
-            {
-                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
-                rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-            }
-            l_run[qs] = l_run[qs] * alpha + rowsum;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[db][qs][i] *= alpha;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int ks = t >> 1, base = 8 * (t & 1);
-                uint4 packed;
-                packed.x = pack2(s[ks][qs][base + 0], s[ks][qs][base + 1]);
-                packed.y = pack2(s[ks][qs][base + 2], s[ks][qs][base + 3]);
-                packed.z = pack2(s[ks][qs][base + 4], s[ks][qs][base + 5]);
-                packed.w = pack2(s[ks][qs][base + 6], s[ks][qs][base + 7]);
-                pop[qs][t] = as_bf16x8(packed);
-            }
-        }
-
-        // ---- O^T += V^T P^T
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16_t *vp = vt + (16 * t + v_row_off) * kRow + 32 * db + v_col_off;
-                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp));
-                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRow));
-                uint4 vv;
-                vv.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
-                vv.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
-                vv.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
-                vv.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
-                const bf16x8_t vop = as_bf16x8(vv);
-#pragma unroll
-                for (int qs = 0; qs < 2; ++qs)
-                    acc[db][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop[qs][t], acc[db][qs], 0, 0, 0);
-            }
-        }
-
+        attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, a.c, krow, half, v_row_off,
+                                v_col_off);
         if (has_next) {
             store_tile(lds_k[buf ^ 1], kreg);
             store_tile(lds_v[buf ^ 1], vreg);
         }
         __syncthreads();
+    }
+    if (full * kBN < a.Sk) {
+        const int buf = full & 1;
+        attend_tile<true, NEG>(lds_k[buf], lds_v[buf], a.Sk - full * kBN, qreg, acc, m_run, l_run, a.c, krow, half,
+                               v_row_off, v_col_off);
     }
 
     // ---- o = acc / denominator, bf16; lane owns one query, dims
