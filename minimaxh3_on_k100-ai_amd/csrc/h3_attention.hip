@@ -106,6 +106,12 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
                 s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
         }
     }
+    // Scores stay in arch VGPRs (the softmax reads them with VALU ops); the
+    // output accumulators stay in AGPRs (only MFMA touches them).
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) asm volatile("" : "+v"(s[ks][qs]));
 
     bf16x8_t pop[2][4];  // P^T operands: query block x 16-key step
 #pragma unroll
@@ -139,10 +145,19 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
             m_run[qs] = m_new;
             l_run[qs] *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+            for (int db = 0; db < 4; ++db) {
+                f32x16_t t = acc[db][qs];
+                asm volatile("" : "+v"(t));
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[db][qs][i] *= alpha;
+                for (int i = 0; i < 16; ++i) t[i] *= alpha;
+                asm volatile("" : "+v"(t));
+                acc[db][qs] = t;
+            }
         }
+        // Keep the accumulators in AGPRs across the (rarely taken) rescale, so
+        // only that path moves them through VGPRs.
+#pragma unroll
+        for (int db = 0; db < 4; ++db) asm volatile("" : "+a"(acc[db][qs]));
         const float m_use = m_run[qs];
         float rowsum = 0.0f;
 #pragma unroll
@@ -224,6 +239,12 @@ __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) qreg[qs][kk] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 16 * kk));
     }
+    // The Q operands are read only by MFMA: park them in AGPRs and leave the
+    // arch VGPRs to the scores and the softmax.
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) asm volatile("" : "+a"(qreg[qs][kk]));
 
     f32x16_t acc[4][2];  // O^T: dim block db (32 dims) x query block qs
 #pragma unroll
