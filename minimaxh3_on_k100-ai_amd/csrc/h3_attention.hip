@@ -37,11 +37,14 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 constexpr int kD = 128;           // head dim
-constexpr int kBM = 256;          // queries per workgroup
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;                     // waves per workgroup (2 per SIMD)
+constexpr int kQS = 1;                        // 32-query MFMA blocks per wave
+constexpr int kThreadsWG = 64 * kWaves;
+constexpr int kBM = 32 * kQS * kWaves;        // queries per workgroup
 constexpr int kBN = 64;           // keys per tile
 constexpr int kRow = kD + 8;      // LDS row pitch in elements (16-byte pad)
 constexpr int kTileElems = kBN * kRow;
+constexpr int kLoadRows = kBN * 16 / kThreadsWG;  // 16-byte chunks per thread per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -64,12 +67,13 @@ __device__ __forceinline__ int xcd_remap(int x, int total) {
 }
 
 // Global -> registers for one 64-key tile of K or V: thread t loads rows
-// t/16 + 16r (r = 0..3), 16-byte chunk t%16. Rows past `valid` are zero.
-__device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid, uint4 reg[4]) {
+// t/16 + (threads/16) r, 16-byte chunk t%16. Rows past `valid` are zero.
+__device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid,
+                                          uint4 reg[kLoadRows]) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = t / 16 + 16 * r;
+    for (int r = 0; r < kLoadRows; ++r) {
+        const int row = t / 16 + (kThreadsWG / 16) * r;
         if (row < valid) {
             reg[r] = *reinterpret_cast<const uint4 *>(base + static_cast<int64_t>(key0 + row) * s_stride + (t % 16) * 8);
         } else {
@@ -78,23 +82,24 @@ __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, 
     }
 }
 
-__device__ __forceinline__ void store_tile(bf16_t *lds, const uint4 reg[4]) {
+__device__ __forceinline__ void store_tile(bf16_t *lds, const uint4 reg[kLoadRows]) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) *reinterpret_cast<uint4 *>(lds + (t / 16 + 16 * r) * kRow + (t % 16) * 8) = reg[r];
+    for (int r = 0; r < kLoadRows; ++r)
+        *reinterpret_cast<uint4 *>(lds + (t / 16 + (kThreadsWG / 16) * r) * kRow + (t % 16) * 8) = reg[r];
 }
 
 // One 64-key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK marks the
 // last, partial tile (keys >= valid are excluded).
 template <bool MASK, bool NEG>
-__device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[2][8],
-                                            f32x16_t (&acc)[4][2], float (&m_run)[2], float (&l_run)[2], float c,
+__device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[kQS][8],
+                                            f32x16_t (&acc)[4][kQS], float (&m_run)[kQS], float (&l_run)[kQS], float c,
                                             int krow, int half, int v_row_off, int v_col_off) {
-    f32x16_t s[2][2];
+    f32x16_t s[2][kQS];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs)
+        for (int qs = 0; qs < kQS; ++qs)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[ks][qs][i] = 0.0f;
 #pragma unroll
@@ -102,7 +107,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
             const bf16x8_t kop =
                 as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRow + 16 * kk + 8 * half));
 #pragma unroll
-            for (int qs = 0; qs < 2; ++qs)
+            for (int qs = 0; qs < kQS; ++qs)
                 s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
         }
     }
@@ -111,11 +116,11 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) asm volatile("" : "+v"(s[ks][qs]));
+        for (int qs = 0; qs < kQS; ++qs) asm volatile("" : "+v"(s[ks][qs]));
 
-    bf16x8_t pop[2][4];  // P^T operands: query block x 16-key step
+    bf16x8_t pop[kQS][4];  // P^T operands: query block x 16-key step
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < kQS; ++qs) {
         if constexpr (MASK) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
@@ -200,14 +205,14 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
             const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
             const bf16x8_t vop = as_bf16x8(make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
 #pragma unroll
-            for (int qs = 0; qs < 2; ++qs)
+            for (int qs = 0; qs < kQS; ++qs)
                 acc[db][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop[qs][t], acc[db][qs], 0, 0, 0);
         }
     }
 }
 
 template <bool NEG>
-__global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElems];
     __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElems];
 
@@ -229,10 +234,10 @@ __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // Q^T operands: query block qs (0/1) of this wave, k-step kk covers dims
     // 16kk + 8*half .. +8.
-    const int q_first = qb * kBM + wave * 64;
-    bf16x8_t qreg[2][8];
+    const int q_first = qb * kBM + wave * 32 * kQS;
+    bf16x8_t qreg[kQS][8];
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < kQS; ++qs) {
         int query = q_first + qs * 32 + l32;
         query = query < a.Sq ? query : a.Sq - 1;
         const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2] + 8 * half;
@@ -242,21 +247,26 @@ __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // The Q operands are read only by MFMA: park them in AGPRs and leave the
     // arch VGPRs to the scores and the softmax.
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs)
+    for (int qs = 0; qs < kQS; ++qs)
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) asm volatile("" : "+a"(qreg[qs][kk]));
 
-    f32x16_t acc[4][2];  // O^T: dim block db (32 dims) x query block qs
+    f32x16_t acc[4][kQS];  // O^T: dim block db (32 dims) x query block qs
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs)
+        for (int qs = 0; qs < kQS; ++qs)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[db][qs][i] = 0.0f;
-    float m_run[2] = {-INFINITY, -INFINITY};  // running max of the logits
-    float l_run[2] = {0.0f, 0.0f};            // running denominator
+    float m_run[kQS];  // running max of the logits
+    float l_run[kQS];
+#pragma unroll
+    for (int qs = 0; qs < kQS; ++qs) {
+        m_run[qs] = -INFINITY;
+        l_run[qs] = 0.0f;  // running denominator
+    }
 
-    uint4 kreg[4], vreg[4];
+    uint4 kreg[kLoadRows], vreg[kLoadRows];
     load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
     load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
     store_tile(lds_k[0], kreg);
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(kBM) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // ---- o = acc / denominator, bf16; lane owns one query, dims
     // 32db + 8g + 4*half + 0..3 for g = 0..3.
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < kQS; ++qs) {
         const int query = q_first + qs * 32 + l32;
         if (query >= a.Sq) continue;
         const float inv = __fdiv_rn(1.0f, l_run[qs]);
@@ -357,8 +367,8 @@ extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, 
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     a.c = static_cast<float>(static_cast<float>(sc) * kLog2e);
     if (a.c < 0.0f)
-        attention_fwd_kernel<true><<<static_cast<unsigned>(grid), kBM, 0, as_stream(stream)>>>(a);
+        attention_fwd_kernel<true><<<static_cast<unsigned>(grid), kThreadsWG, 0, as_stream(stream)>>>(a);
     else
-        attention_fwd_kernel<false><<<static_cast<unsigned>(grid), kBM, 0, as_stream(stream)>>>(a);
+        attention_fwd_kernel<false><<<static_cast<unsigned>(grid), kThreadsWG, 0, as_stream(stream)>>>(a);
     return launch_status();
 }
