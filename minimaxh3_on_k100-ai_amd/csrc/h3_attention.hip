@@ -3,12 +3,16 @@
 // (tools/h3_attention.py:25-41, `fp32_qk` numerics).
 //
 // Work decomposition
-//   - one 256-thread workgroup per (batch, head, 256-query block); the
-//     workgroup order is remapped so the blocks dispatched to one XCD are
-//     consecutive (same head), sharing that XCD's L2 for the K/V stream;
-//   - each wave owns 64 queries as two 32-query MFMA blocks and keeps its Q^T
-//     operands in registers for the whole key loop;
-//   - K/V tiles of 64 keys are staged in double-buffered LDS.
+//   - one 512-thread workgroup (8 waves, two per SIMD) per (batch, head,
+//     256-query block); the workgroup order is remapped so the blocks
+//     dispatched to one XCD are consecutive (same head) and share that XCD's
+//     L2 for the K/V stream;
+//   - each wave owns 32 queries and keeps its Q^T operands in registers for
+//     the whole key loop; all of a wave's state (Q, scores, O accumulators)
+//     lives in arch VGPRs (174 of the 256 a wave gets at two waves per SIMD),
+//     so the softmax never shuttles values through AGPRs;
+//   - K/V tiles of 64 keys are staged in double-buffered LDS with
+//     bank-conflict-free pitches (below).
 //
 // MFMA formulation (v_mfma_f32_32x32x16_bf16; A row = lane % 32, B column =
 // lane % 32, accumulator register i of lane l holds row 8*(i/4) + 4*(l/32) + i%4)
@@ -42,8 +46,15 @@ constexpr int kQS = 1;                        // 32-query MFMA blocks per wave
 constexpr int kThreadsWG = 64 * kWaves;
 constexpr int kBM = 32 * kQS * kWaves;        // queries per workgroup
 constexpr int kBN = 64;           // keys per tile
-constexpr int kRow = kD + 8;      // LDS row pitch in elements (16-byte pad)
-constexpr int kTileElems = kBN * kRow;
+// LDS row pitches (elements), chosen against 64 banks x 4 bytes:
+//   K: 272 B -> the 16 rows read by one 16-lane ds_read_b128 pass start 4
+//      banks apart and cover every bank once;
+//   V: 320 B -> the 4 rows x 16 dims of each 16-lane ds_read_b64_tr_b16
+//      group start 16 banks apart, so a 32-lane pass covers every bank once.
+constexpr int kRowK = kD + 8;
+constexpr int kRowV = kD + 32;
+constexpr int kTileElemsK = kBN * kRowK;
+constexpr int kTileElemsV = kBN * kRowV;
 constexpr int kLoadRows = kBN * 16 / kThreadsWG;  // 16-byte chunks per thread per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -82,11 +93,12 @@ __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, 
     }
 }
 
+template <int PITCH>
 __device__ __forceinline__ void store_tile(bf16_t *lds, const uint4 reg[kLoadRows]) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r)
-        *reinterpret_cast<uint4 *>(lds + (t / 16 + (kThreadsWG / 16) * r) * kRow + (t % 16) * 8) = reg[r];
+        *reinterpret_cast<uint4 *>(lds + (t / 16 + (kThreadsWG / 16) * r) * PITCH + (t % 16) * 8) = reg[r];
 }
 
 // One 64-key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK marks the
@@ -105,18 +117,21 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
             const bf16x8_t kop =
-                as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRow + 16 * kk + 8 * half));
+                as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRowK + 16 * kk + 8 * half));
 #pragma unroll
             for (int qs = 0; qs < kQS; ++qs)
                 s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
         }
     }
-    // Scores stay in arch VGPRs (the softmax reads them with VALU ops); the
-    // output accumulators stay in AGPRs (only MFMA touches them).
+    // Rolling window of K operand reads: two reads ahead of the MFMAs, so only
+    // a few operands occupy VGPRs at any time.
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int qs = 0; qs < kQS; ++qs) asm volatile("" : "+v"(s[ks][qs]));
+    for (int i = 0; i < 14; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kQS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kQS, 0);
 
     bf16x8_t pop[kQS][4];  // P^T operands: query block x 16-key step
 #pragma unroll
@@ -150,19 +165,10 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
             m_run[qs] = m_new;
             l_run[qs] *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                f32x16_t t = acc[db][qs];
-                asm volatile("" : "+v"(t));
+            for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) t[i] *= alpha;
-                asm volatile("" : "+v"(t));
-                acc[db][qs] = t;
-            }
+                for (int i = 0; i < 16; ++i) acc[db][qs][i] *= alpha;
         }
-        // Keep the accumulators in AGPRs across the (rarely taken) rescale, so
-        // only that path moves them through VGPRs.
-#pragma unroll
-        for (int db = 0; db < 4; ++db) asm volatile("" : "+a"(acc[db][qs]));
         const float m_use = m_run[qs];
         float rowsum = 0.0f;
 #pragma unroll
@@ -199,9 +205,9 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            const bf16_t *vp = vt + (16 * t + v_row_off) * kRow + 32 * db + v_col_off;
+            const bf16_t *vp = vt + (16 * t + v_row_off) * kRowV + 32 * db + v_col_off;
             const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp));
-            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRow));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRowV));
             const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
             const bf16x8_t vop = as_bf16x8(make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
 #pragma unroll
@@ -209,12 +215,21 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
                 acc[db][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop[qs][t], acc[db][qs], 0, 0, 0);
         }
     }
+    // Rolling window of V^T operand reads (two ds_read_b64_tr_b16 per MFMA
+    // operand), two operands ahead of the MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kQS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kQS, 0);
 }
 
 template <bool NEG>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElems];
-    __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElems];
+    __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElemsK];
+    __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElemsV];
 
     const int total = a.B * a.H * a.qblocks;
     const int logical = xcd_remap(blockIdx.x, total);
@@ -244,12 +259,6 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) qreg[qs][kk] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 16 * kk));
     }
-    // The Q operands are read only by MFMA: park them in AGPRs and leave the
-    // arch VGPRs to the scores and the softmax.
-#pragma unroll
-    for (int qs = 0; qs < kQS; ++qs)
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) asm volatile("" : "+a"(qreg[qs][kk]));
 
     f32x16_t acc[4][kQS];  // O^T: dim block db (32 dims) x query block qs
 #pragma unroll
@@ -269,8 +278,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     uint4 kreg[kLoadRows], vreg[kLoadRows];
     load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
     load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
-    store_tile(lds_k[0], kreg);
-    store_tile(lds_v[0], vreg);
+    store_tile<kRowK>(lds_k[0], kreg);
+    store_tile<kRowV>(lds_v[0], vreg);
     __syncthreads();
 
     // K row read by MFMA row m (bits 2 and 3 swapped).
@@ -295,8 +304,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, a.c, krow, half, v_row_off,
                                 v_col_off);
         if (has_next) {
-            store_tile(lds_k[buf ^ 1], kreg);
-            store_tile(lds_v[buf ^ 1], vreg);
+            store_tile<kRowK>(lds_k[buf ^ 1], kreg);
+            store_tile<kRowV>(lds_v[buf ^ 1], vreg);
         }
         __syncthreads();
     }
