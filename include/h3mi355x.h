@@ -54,22 +54,27 @@ NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothed
                                            NineToothedTensor k, NineToothedTensor v,
                                            NineToothedTensor scale, NineToothedTensor o);
 
-/* Per-head fp8 (OCP e4m3fn) quantisation for the fp8 attention variant.
- * x: bf16 [B, H, S, 128] (any strides on B/H/S, unit stride on D);
- * x8: uint8 storage of e4m3fn, same shape; descale: fp32 [H] (contiguous),
- * receives amax_h / 448, the factor that maps x8 back to x. A head with
- * amax 0 gets descale 1 and all-zero codes.
+/* Per-head fp8 (OCP e4m3fn) quantisation for the fp8 attention variants.
+ * x: bf16 [B, H, S, 128] (any strides on B/H/S, unit stride on D, 16-byte
+ * aligned rows); x8: uint8 storage of e4m3fn codes, same shape, either
+ * D-contiguous (16-byte rows) or S-contiguous (the V^T layout the attention
+ * kernels read V in; its D stride a multiple of 16); descale: fp32 [H]
+ * (contiguous), receives amax_h / 448, the factor that maps x8 back to x.
+ * A head with amax 0 gets descale 1 and all-zero codes. The kernel chain
+ * clears, then accumulates, the amax in `descale` itself (no workspace).
  * No counterpart in the reference (it has no fp8 path); its callers are the
  * fp8 attention users below. */
 NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, NineToothedTensor x,
                                                   NineToothedTensor x8, NineToothedTensor descale);
 
-/* fp8 (OCP e4m3fn) non-causal attention forward with per-head descales.
- * q8, k8, v8: uint8 e4m3fn [B, H, S, 128] (unit stride on D, 16-byte aligned
- * rows); q_descale, k_descale, v_descale: fp32 [H]; scale: fp64 scalar;
- * o: bf16 [B, H, Sq, 128]. Logits accumulate in fp32 on the fp8 MFMA; P is
- * requantised per tile to e4m3fn with the fixed factor 448 (P <= 1 after the
- * running-max shift); the fp32 P.V accumulator is rescaled by v_descale/448.
+/* fp8 (OCP e4m3fn) non-causal attention with per-head descales: the all-fp8
+ * recipe. q8, k8: uint8 e4m3fn [B, H, S, 128] (unit stride on D, 16-byte
+ * aligned rows); v8: uint8 e4m3fn [B, H, Sk, 128] with unit stride on S (see
+ * the quantiser); q_descale, k_descale, v_descale: fp32 [H]; scale: fp64;
+ * o: bf16 [B, H, Sq, 128]. Logits = (q8 . k8) q_descale k_descale scale in
+ * fp32 on the fp8 MFMA; P is requantised per 64-key tile to e4m3(448 P)
+ * (P <= 1 after the running-max shift); the fp32 P.V accumulator is scaled by
+ * v_descale / 448 and divided by the fp32 denominator.
  * No counterpart in the reference (fp8 attention is a new feature); same
  * callers as launch_h3_full_attention. */
 NineToothedResult launch_h3_full_attention_fp8(NineToothedStream stream, NineToothedTensor q8,
@@ -77,6 +82,16 @@ NineToothedResult launch_h3_full_attention_fp8(NineToothedStream stream, NineToo
                                                NineToothedTensor q_descale, NineToothedTensor k_descale,
                                                NineToothedTensor v_descale, NineToothedTensor scale,
                                                NineToothedTensor o);
+
+/* fp8 P.V with bf16 logits: q, k bf16 [B, H, S, 128] as for
+ * launch_h3_full_attention, v8 and v_descale as for
+ * launch_h3_full_attention_fp8. Keeps the Q K^T product (whose e4m3 error
+ * grows with the logit magnitude) in bf16 and runs only P.V on the fp8 MFMA.
+ * No counterpart in the reference; same callers as launch_h3_full_attention. */
+NineToothedResult launch_h3_full_attention_fp8pv(NineToothedStream stream, NineToothedTensor q,
+                                                 NineToothedTensor k, NineToothedTensor v8,
+                                                 NineToothedTensor v_descale, NineToothedTensor scale,
+                                                 NineToothedTensor o);
 
 /* ---------------------------------------------------------------- pointwise */
 

@@ -8,7 +8,12 @@ and the `h3_pointwise.make_*` functions. The package name is not a Python
 identifier; import it with importlib.import_module("minimaxh3_on_k100-ai_amd").
 """
 from . import _lib, h3_attention, h3_pointwise  # noqa: F401
-from .h3_attention import make_attention, make_attention_fp8, quantize_fp8_per_head  # noqa: F401
+from .h3_attention import (  # noqa: F401
+    make_attention,
+    make_attention_fp8,
+    make_attention_fp8pv,
+    quantize_fp8_per_head,
+)
 from .h3_pointwise import (  # noqa: F401
     make_gated_residual,
     make_gated_residual_rms_modulate,

@@ -1,0 +1,587 @@
+// fp8 (OCP e4m3fn) attention for gfx950: per-head quantisation of Q/K/V and a
+// flash-attention forward whose P.V product (and, in the all-fp8 recipe, the
+// Q K^T product) runs on v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales).
+// No counterpart in the reference, which has no fp8 path; the numerics follow
+// its bf16 kernel (tools/h3_attention.py:25-41) with these changes:
+//   - x8 = e4m3(x * 448 / amax_h), descale_h = amax_h / 448 per head;
+//   - logits = (q8 . k8) * q_descale * k_descale * scale * log2(e) (all-fp8), or
+//     the bf16 logits of the bf16 kernel (fp8 P.V variant);
+//   - P = exp2(logit - running max) is requantised per 64-key tile as
+//     e4m3(448 * P) (P <= 1, so the fixed factor uses the whole range); the
+//     denominator sums the unquantised fp32 P; o = acc * v_descale / (448 l).
+//
+// Work decomposition as in the bf16 kernel: 512-thread workgroups (8 waves,
+// two per SIMD), 32 queries per wave, 64-key tiles in double-buffered LDS,
+// S^T = K Q^T so each lane owns one query row of the softmax.
+//
+// Key order. K row for MFMA row m of 32-key block ks is
+//   key(ks, m) = 32*bit2(m) + 16*ks + 4*(m >> 3) + (m & 3),
+// which makes accumulator register i of block ks in a lane of half h hold key
+// 32h + 16ks + i: each lane's 32 scores are the contiguous keys [32h, 32h+32)
+// of the tile, i.e. exactly the 32 k-slots of its half in the 64-deep fp8 P.V
+// MFMA. The V operand is then V^T[d][32h .. 32h+32): 32 contiguous bytes of
+// the V^T tile, which the quantiser provides by writing V8 S-contiguous.
+//
+// LDS tiles carry no padding; 16-byte chunks are XOR-swizzled per row so the
+// rows read by one 16-lane ds_read_b128 pass fall in distinct banks.
+#include "h3_common.hpp"
+
+namespace h3 {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kD = 128;
+constexpr int kWaves = 8;
+constexpr int kThreadsWG = 64 * kWaves;
+constexpr int kBM = 32 * kWaves;
+constexpr int kBN = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kE4M3Max = 448.0f;
+constexpr int kScale1 = 127;  // E8M0 exponent of 1.0 for the scaled MFMA
+
+// ------------------------------------------------------------------ swizzles
+
+// K tile of QK_FP8 (fp8, 128 B rows = 8 chunks): position of chunk c of row r.
+__device__ __forceinline__ int kswz8(int r, int c) { return c ^ (((r >> 1) & 3) | (((r >> 5) & 1) << 2)); }
+// K tile of bf16 logits (256 B rows = 16 chunks).
+__device__ __forceinline__ int kswz16(int r, int c) { return c ^ ((r & 7) | (((r >> 5) & 1) << 3)); }
+// V^T tile (64 B rows = 4 chunks).
+__device__ __forceinline__ int vswz(int d, int c) { return c ^ ((d >> 2) & 3); }
+
+// K row feeding MFMA row m of 32-key block ks (see header).
+__device__ __forceinline__ int key_of_row(int ks, int m) {
+    return 32 * ((m >> 2) & 1) + 16 * ks + 4 * (m >> 3) + (m & 3);
+}
+
+__device__ __forceinline__ int xcd_remap(int x, int total) {
+    const int per = total / 8, rem = total % 8;
+    const int xcd = x % 8, slot = x / 8;
+    return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+struct Fp8Args {
+    const uint8_t *q8, *k8;  // all-fp8 recipe
+    const bf16_t *q, *k;     // bf16-logit variant
+    const uint8_t *v8;       // S-contiguous (element (b, h, s, d) at b*vs0 + h*vs1 + s + d*vs3)
+    bf16_t *o;
+    const float *q_descale, *k_descale, *v_descale;
+    int64_t qs[3], ks[3], vs0, vs1, vs3, os[3];
+    int B, H, Sq, Sk, qblocks;
+    float c;  // scale * log2(e)
+};
+
+// ------------------------------------------------------------------ tiles
+
+// K tile, global -> LDS (through registers): 64 rows of 128 (fp8) or 256 (bf16)
+// bytes; rows past `valid` are zero.
+template <bool QK_FP8>
+__device__ __forceinline__ void load_k(const Fp8Args &a, int b, int h, int key0, int valid, uint4 (&reg)[2]) {
+    const int t = threadIdx.x;
+    constexpr int kChunks = QK_FP8 ? 8 : 16;
+    constexpr int kPerThread = kBN * kChunks / kThreadsWG;  // 1 or 2
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int idx = t + i * kThreadsWG;
+        const int r = idx / kChunks, c = idx % kChunks;
+        if (r < valid) {
+            const uint8_t *row = QK_FP8
+                ? a.k8 + b * a.ks[0] + h * a.ks[1] + static_cast<int64_t>(key0 + r) * a.ks[2]
+                : reinterpret_cast<const uint8_t *>(a.k + b * a.ks[0] + h * a.ks[1] +
+                                                    static_cast<int64_t>(key0 + r) * a.ks[2]);
+            reg[i] = *reinterpret_cast<const uint4 *>(row + 16 * c);
+        } else {
+            reg[i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+template <bool QK_FP8>
+__device__ __forceinline__ void store_k(uint8_t *lds, const uint4 (&reg)[2]) {
+    const int t = threadIdx.x;
+    constexpr int kChunks = QK_FP8 ? 8 : 16;
+    constexpr int kPerThread = kBN * kChunks / kThreadsWG;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int idx = t + i * kThreadsWG;
+        const int r = idx / kChunks, c = idx % kChunks;
+        const int pos = QK_FP8 ? kswz8(r, c) : kswz16(r, c);
+        *reinterpret_cast<uint4 *>(lds + r * (16 * kChunks) + 16 * pos) = reg[i];
+    }
+}
+
+// V^T tile: 128 rows (dims) of 64 key bytes; keys past `valid` are zero.
+__device__ __forceinline__ void load_v(const Fp8Args &a, int b, int h, int key0, int valid, uint4 &reg) {
+    const int t = threadIdx.x;
+    const int d = t / 4, c = t % 4;
+    const uint8_t *row = a.v8 + b * a.vs0 + h * a.vs1 + static_cast<int64_t>(d) * a.vs3 + key0 + 16 * c;
+    if (16 * c + 16 <= valid) {
+        reg = *reinterpret_cast<const uint4 *>(row);
+    } else {
+        uint8_t bytes[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) bytes[e] = (16 * c + e < valid) ? row[e] : 0;
+        reg = *reinterpret_cast<const uint4 *>(bytes);
+    }
+}
+
+__device__ __forceinline__ void store_v(uint8_t *lds, const uint4 &reg) {
+    const int t = threadIdx.x;
+    const int d = t / 4, c = t % 4;
+    *reinterpret_cast<uint4 *>(lds + d * 64 + 16 * vswz(d, c)) = reg;
+}
+
+// ------------------------------------------------------------------ kernel
+
+template <bool QK_FP8, bool NEG>
+__global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fp8_kernel(
+    Fp8Args a) {
+    constexpr int kKBytes = kBN * (QK_FP8 ? 128 : 256);
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kKBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kD * kBN];
+
+    const int total = a.B * a.H * a.qblocks;
+    const int logical = xcd_remap(blockIdx.x, total);
+    const int qb = logical % a.qblocks;
+    const int bh = logical / a.qblocks;
+    const int b = bh / a.H, h = bh % a.H;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int l32 = lane & 31;
+    const int half = lane >> 5;
+
+    const float c = QK_FP8 ? a.c * a.q_descale[h] * a.k_descale[h] : a.c;
+    const float out_scale = a.v_descale[h] / kE4M3Max;
+
+    // Q^T operands (this lane's query row).
+    const int query = qb * kBM + wave * 32 + l32;
+    const int qrow_i = query < a.Sq ? query : a.Sq - 1;
+    i32x8_t q8reg[2];
+    bf16x8_t qbreg[8];
+    if constexpr (QK_FP8) {
+        const uint8_t *qrow = a.q8 + b * a.qs[0] + h * a.qs[1] + static_cast<int64_t>(qrow_i) * a.qs[2] + 32 * half;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const uint4 lo = *reinterpret_cast<const uint4 *>(qrow + 64 * kk);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(qrow + 64 * kk + 16);
+            q8reg[kk] = i32x8_t{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                                static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                static_cast<int>(hi.z), static_cast<int>(hi.w)};
+        }
+    } else {
+        const bf16_t *qrow = a.q + b * a.qs[0] + h * a.qs[1] + static_cast<int64_t>(qrow_i) * a.qs[2] + 8 * half;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            qbreg[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(qrow + 16 * kk));
+    }
+
+    f32x16_t acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int ntiles = (a.Sk + kBN - 1) / kBN;
+    {
+        uint4 kr[2], vr;
+        const int valid = a.Sk < kBN ? a.Sk : kBN;
+        load_k<QK_FP8>(a, b, h, 0, valid, kr);
+        load_v(a, b, h, 0, valid, vr);
+        store_k<QK_FP8>(lds_k[0], kr);
+        store_v(lds_v[0], vr);
+    }
+    __syncthreads();
+
+    for (int tile = 0; tile < ntiles; ++tile) {
+        const int buf = tile & 1;
+        const int key0 = tile * kBN;
+        const int valid = a.Sk - key0 < kBN ? a.Sk - key0 : kBN;
+        const bool has_next = tile + 1 < ntiles;
+        uint4 kr[2], vr;
+        if (has_next) {
+            const int nvalid = a.Sk - key0 - kBN < kBN ? a.Sk - key0 - kBN : kBN;
+            load_k<QK_FP8>(a, b, h, key0 + kBN, nvalid, kr);
+            load_v(a, b, h, key0 + kBN, nvalid, vr);
+        }
+        const uint8_t *kt = lds_k[buf];
+        const uint8_t *vt = lds_v[buf];
+
+        // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
+        f32x16_t s[2];
+        const f32x16_t zero = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int r = key_of_row(ks, l32);
+            if constexpr (QK_FP8) {
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int c0 = 4 * kk + 2 * half;  // 16-byte chunk of dims 64kk + 32half
+                    const uint4 lo = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0));
+                    const uint4 hi = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0 + 1));
+                    const i32x8_t kop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                                      static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                      static_cast<int>(hi.z), static_cast<int>(hi.w)};
+                    s[ks] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q8reg[kk], kk == 0 ? zero : s[ks], 0,
+                                                                            0, 0, kScale1, 0, kScale1);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                    const int c0 = 2 * kk + half;  // 16-byte chunk of dims 16kk + 8half
+                    const bf16x8_t kop =
+                        __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(kt + r * 256 + 16 * kswz16(r, c0)));
+                    s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qbreg[kk], kk == 0 ? zero : s[ks], 0, 0, 0);
+                }
+            }
+        }
+
+        // ---- online softmax (this lane's query)
+        const bool masked = valid < kBN;
+        if (masked) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (32 * half + 16 * ks + i >= valid) s[ks][i] = NEG ? INFINITY : -INFINITY;
+        }
+        float mx = s[0][0];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][i]) : fmaxf(mx, s[ks][i]);
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
+            mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
+        }
+        const float m_tile = mx * c;
+        const bool grow = m_tile > m_run;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float m_new = grow ? m_tile : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+        }
+        float rowsum = 0.0f;
+        int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
+                if (masked && 32 * half + 16 * ks + i >= valid) p = 0.0f;
+                s[ks][i] = p;
+                rowsum += p;
+            }
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
+                v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
+                pk[4 * ks + w] = v;
+            }
+        }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
+            rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        l_run += rowsum;
+        const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
+
+        // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 32 * db + l32;
+            const uint4 lo = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half));
+            const uint4 hi = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half + 1));
+            const i32x8_t vop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                              static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                              static_cast<int>(hi.z), static_cast<int>(hi.w)};
+            acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, pop, acc[db], 0, 0, 0, kScale1, 0, kScale1);
+        }
+
+        if (has_next) {
+            store_k<QK_FP8>(lds_k[buf ^ 1], kr);
+            store_v(lds_v[buf ^ 1], vr);
+        }
+        __syncthreads();
+    }
+
+    if (query >= a.Sq) return;
+    const float inv = out_scale / l_run;
+    bf16_t *orow = a.o + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(query) * a.os[2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint2 w;
+            w.x = pack2(acc[db][4 * g + 0] * inv, acc[db][4 * g + 1] * inv);
+            w.y = pack2(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv);
+            *reinterpret_cast<uint2 *>(orow + 32 * db + 8 * g + 4 * half) = w;
+        }
+}
+
+// ------------------------------------------------------------------ quantiser
+
+// descale[h] <- 0 (amax accumulator, as uint bits of a non-negative float).
+__global__ void zero_kernel(float *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+// amax[h] = max |x[:, h, :, :]|; 16 threads per 128-element row, 256 rows per block.
+__global__ __launch_bounds__(256) void amax_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2, int B, int S,
+                                                   int rows_per_block, float *amax) {
+    const int h = blockIdx.y;
+    const int64_t rows = static_cast<int64_t>(B) * S;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+    uint32_t m = 0;
+    for (int64_t r = r0 + threadIdx.x / 16; r < r0 + rows_per_block && r < rows; r += 16) {
+        const int64_t bb = r / S, ss = r % S;
+        const U4 v = ld16(x + bb * s0 + h * s1 + ss * s2 + 8 * (threadIdx.x % 16));
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = (w[e] << 16) & 0x7fffffffu, hi = w[e] & 0x7fff0000u;
+            m = lo > m ? lo : m;
+            m = hi > m ? hi : m;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(reinterpret_cast<unsigned int *>(amax) + h, m);
+}
+
+__device__ __forceinline__ uint32_t quant4(const float f[4], float inv) {
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = fminf(fmaxf(f[e] * inv, -kE4M3Max), kE4M3Max);
+    int v = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], v, true);
+    return static_cast<uint32_t>(v);
+}
+
+// x8 = e4m3(x * 448 / amax_h). D-contiguous output: 16 dims per thread.
+__global__ __launch_bounds__(256) void quant_rows_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2,
+                                                         uint8_t *y, int64_t t0, int64_t t1, int64_t t2, int B, int H,
+                                                         int S, const float *amax) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (row, 16-dim chunk)
+    const int64_t n = static_cast<int64_t>(B) * H * S * 8;
+    if (i >= n) return;
+    const int chunk = static_cast<int>(i % 8);
+    const int64_t row = i / 8;
+    const int64_t ss = row % S, bh = row / S;
+    const int hh = static_cast<int>(bh % H);
+    const int64_t bb = bh / H;
+    const float a = amax[hh];
+    const float inv = a > 0.0f ? kE4M3Max / a : 0.0f;
+    const bf16_t *src = x + bb * s0 + hh * s1 + ss * s2 + 16 * chunk;
+    float f[16];
+    u4_to_f8(ld16(src), f);
+    u4_to_f8(ld16(src + 8), f + 8);
+    uint4 out;
+    out.x = quant4(f, inv);
+    out.y = quant4(f + 4, inv);
+    out.z = quant4(f + 8, inv);
+    out.w = quant4(f + 12, inv);
+    *reinterpret_cast<uint4 *>(y + bb * t0 + hh * t1 + ss * t2 + 16 * chunk) = out;
+}
+
+// x8 = e4m3(x * 448 / amax_h) written S-contiguous (V^T layout): a 64-token x
+// 128-dim tile per block, transposed through LDS.
+__global__ __launch_bounds__(256) void quant_transposed_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2,
+                                                               uint8_t *y, int64_t t0, int64_t t1, int64_t t3, int H,
+                                                               int S, int stiles, const float *amax) {
+    __shared__ uint8_t tile[kD][64 + 4];
+    const int st = blockIdx.x % stiles;
+    const int bh = blockIdx.x / stiles;
+    const int hh = bh % H, bb = bh / H;
+    const int s_base = st * 64;
+    const float a = amax[hh];
+    const float inv = a > 0.0f ? kE4M3Max / a : 0.0f;
+    // Read: 64 rows x 16 chunks of 8 dims; thread t handles chunks t, t+256, t+512, t+768.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int idx = threadIdx.x + 256 * k;
+        const int r = idx / 16, ch = idx % 16;
+        float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (s_base + r < S) u4_to_f8(ld16(x + bb * s0 + hh * s1 + static_cast<int64_t>(s_base + r) * s2 + 8 * ch), f);
+        const uint32_t lo = quant4(f, inv), hi = quant4(f + 4, inv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            tile[8 * ch + e][r] = static_cast<uint8_t>(lo >> (8 * e));
+            tile[8 * ch + 4 + e][r] = static_cast<uint8_t>(hi >> (8 * e));
+        }
+    }
+    __syncthreads();
+    // Write: 128 dims x 64 tokens; thread t writes 32 tokens of dim t/2.
+    const int d = threadIdx.x / 2, part = threadIdx.x % 2;
+    uint8_t *dst = y + bb * t0 + hh * t1 + static_cast<int64_t>(d) * t3 + s_base + 32 * part;
+    for (int e = 0; e < 32; ++e)
+        if (s_base + 32 * part + e < S) dst[e] = tile[d][32 * part + e];
+}
+
+// descale[h] = amax_h / 448 (1 for an all-zero head).
+__global__ void finalize_kernel(float *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = p[i] > 0.0f ? p[i] / kE4M3Max : 1.0f;
+}
+
+template <bool QK_FP8>
+int launch_fp8(hipStream_t stream, const Fp8Args &a0) {
+    Fp8Args a = a0;
+    a.qblocks = (a.Sq + kBM - 1) / kBM;
+    const int64_t grid = static_cast<int64_t>(a.B) * a.H * a.qblocks;
+    if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
+    if (a.c < 0.0f)
+        attention_fp8_kernel<QK_FP8, true><<<static_cast<unsigned>(grid), kThreadsWG, 0, stream>>>(a);
+    else
+        attention_fp8_kernel<QK_FP8, false><<<static_cast<unsigned>(grid), kThreadsWG, 0, stream>>>(a);
+    return launch_status();
+}
+
+// Shared host checks: o [B, H, Sq, 128] bf16 (D unit-stride, 16-byte rows);
+// v8 [B, H, Sk, 128] with unit stride on S; descales [H] contiguous.
+int check_common(const View<4> &qshape, const View<4> &kshape, const View<4> &v8, const View<4> &o,
+                 const View<1> *descales[], int ndescale, Fp8Args &a) {
+    if (!same_shape(qshape, o) || !same_shape(kshape, v8)) return kInvalid;
+    if (qshape.shape[0] != kshape.shape[0] || qshape.shape[1] != kshape.shape[1] || qshape.shape[3] != kD ||
+        kshape.shape[3] != kD)
+        return kInvalid;
+    if (!rows_vec16(o, 2)) return kInvalid;
+    if (v8.shape[2] > 1 && v8.stride[2] != 1) return kInvalid;
+    if ((reinterpret_cast<uintptr_t>(v8.data) & 15) != 0 || (v8.stride[3] % 16) != 0 ||
+        (v8.shape[0] > 1 && v8.stride[0] % 16 != 0) || (v8.shape[1] > 1 && v8.stride[1] % 16 != 0))
+        return kInvalid;
+    for (int i = 0; i < ndescale; ++i) {
+        const View<1> &d = *descales[i];
+        if (d.shape[0] != qshape.shape[1] || (d.shape[0] > 1 && d.stride[0] != 1)) return kInvalid;
+    }
+    a.v8 = reinterpret_cast<const uint8_t *>(v8.data);
+    a.vs0 = v8.stride[0];
+    a.vs1 = v8.stride[1];
+    a.vs3 = v8.stride[3];
+    a.o = reinterpret_cast<bf16_t *>(o.data);
+    for (int i = 0; i < 3; ++i) a.os[i] = o.stride[i];
+    a.B = static_cast<int>(qshape.shape[0]);
+    a.H = static_cast<int>(qshape.shape[1]);
+    a.Sq = static_cast<int>(qshape.shape[2]);
+    a.Sk = static_cast<int>(kshape.shape[2]);
+    return 0;
+}
+
+}  // namespace
+}  // namespace h3
+
+using namespace h3;
+
+extern "C" {
+
+NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, NineToothedTensor x,
+                                                  NineToothedTensor x8, NineToothedTensor descale) {
+    View<4> xv, yv;
+    View<1> dv;
+    if (!load_view(x, 2, xv) || !load_view(x8, 1, yv) || !load_view(descale, 4, dv)) return kInvalid;
+    if (!same_shape(xv, yv) || xv.shape[3] != kD || dv.shape[0] != xv.shape[1]) return kInvalid;
+    if (dv.shape[0] > 1 && dv.stride[0] != 1) return kInvalid;
+    if (!rows_vec16(xv, 2)) return kInvalid;
+    const int B = static_cast<int>(xv.shape[0]), H = static_cast<int>(xv.shape[1]), S = static_cast<int>(xv.shape[2]);
+    if (H == 0) return 0;
+    const bool d_contig = rows_vec16(yv, 1);
+    const bool s_contig = (S <= 1 || yv.stride[2] == 1) && (reinterpret_cast<uintptr_t>(yv.data) & 15) == 0 &&
+                          yv.stride[3] % 16 == 0 && (B <= 1 || yv.stride[0] % 16 == 0) &&
+                          (H <= 1 || yv.stride[1] % 16 == 0);
+    if (!d_contig && !s_contig) return kInvalid;
+    hipStream_t st = as_stream(stream);
+    float *amax = reinterpret_cast<float *>(dv.data);
+    zero_kernel<<<(H + 255) / 256, 256, 0, st>>>(amax, H);
+    if (static_cast<int64_t>(B) * S > 0) {
+        const int rows_per_block = 256;
+        const int64_t chunks = (static_cast<int64_t>(B) * S + rows_per_block - 1) / rows_per_block;
+        if (chunks > 65535 * 1024) return kInvalid;
+        amax_kernel<<<dim3(static_cast<unsigned>(chunks), H), 256, 0, st>>>(
+            reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2], B, S, rows_per_block,
+            amax);
+        if (d_contig) {
+            const int64_t n = static_cast<int64_t>(B) * H * S * 8;
+            quant_rows_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(
+                reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2],
+                reinterpret_cast<uint8_t *>(yv.data), yv.stride[0], yv.stride[1], yv.stride[2], B, H, S, amax);
+        } else {
+            const int stiles = (S + 63) / 64;
+            quant_transposed_kernel<<<static_cast<unsigned>(static_cast<int64_t>(B) * H * stiles), 256, 0, st>>>(
+                reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2],
+                reinterpret_cast<uint8_t *>(yv.data), yv.stride[0], yv.stride[1], yv.stride[3], H, S, stiles, amax);
+        }
+    }
+    finalize_kernel<<<(H + 255) / 256, 256, 0, st>>>(amax, H);
+    return launch_status();
+}
+
+NineToothedResult launch_h3_full_attention_fp8(NineToothedStream stream, NineToothedTensor q8, NineToothedTensor k8,
+                                               NineToothedTensor v8, NineToothedTensor q_descale,
+                                               NineToothedTensor k_descale, NineToothedTensor v_descale,
+                                               NineToothedTensor scale, NineToothedTensor o) {
+    View<4> qv, kv, vv, ov;
+    View<1> qd, kd, vd;
+    double sc;
+    if (!load_view(q8, 1, qv) || !load_view(k8, 1, kv) || !load_view(v8, 1, vv) || !load_view(o, 2, ov) ||
+        !load_view(q_descale, 4, qd) || !load_view(k_descale, 4, kd) || !load_view(v_descale, 4, vd) ||
+        !load_scalar(scale, sc))
+        return kInvalid;
+    Fp8Args a{};
+    const View<1> *ds[3] = {&qd, &kd, &vd};
+    if (check_common(qv, kv, vv, ov, ds, 3, a) != 0) return kInvalid;
+    if (!rows_vec16(qv, 1) || !rows_vec16(kv, 1)) return kInvalid;
+    if (qv.shape[0] == 0 || qv.shape[1] == 0 || qv.shape[2] == 0) return 0;
+    if (kv.shape[2] == 0) return kInvalid;
+    a.q8 = reinterpret_cast<const uint8_t *>(qv.data);
+    a.k8 = reinterpret_cast<const uint8_t *>(kv.data);
+    for (int i = 0; i < 3; ++i) {
+        a.qs[i] = qv.stride[i];
+        a.ks[i] = kv.stride[i];
+    }
+    a.q_descale = reinterpret_cast<const float *>(qd.data);
+    a.k_descale = reinterpret_cast<const float *>(kd.data);
+    a.v_descale = reinterpret_cast<const float *>(vd.data);
+    a.c = static_cast<float>(static_cast<float>(sc) * kLog2e);
+    return launch_fp8<true>(as_stream(stream), a);
+}
+
+NineToothedResult launch_h3_full_attention_fp8pv(NineToothedStream stream, NineToothedTensor q, NineToothedTensor k,
+                                                 NineToothedTensor v8, NineToothedTensor v_descale,
+                                                 NineToothedTensor scale, NineToothedTensor o) {
+    View<4> qv, kv, vv, ov;
+    View<1> vd;
+    double sc;
+    if (!load_view(q, 2, qv) || !load_view(k, 2, kv) || !load_view(v8, 1, vv) || !load_view(o, 2, ov) ||
+        !load_view(v_descale, 4, vd) || !load_scalar(scale, sc))
+        return kInvalid;
+    Fp8Args a{};
+    const View<1> *ds[1] = {&vd};
+    if (check_common(qv, kv, vv, ov, ds, 1, a) != 0) return kInvalid;
+    if (!rows_vec16(qv, 2) || !rows_vec16(kv, 2)) return kInvalid;
+    if (qv.shape[0] == 0 || qv.shape[1] == 0 || qv.shape[2] == 0) return 0;
+    if (kv.shape[2] == 0) return kInvalid;
+    a.q = reinterpret_cast<const bf16_t *>(qv.data);
+    a.k = reinterpret_cast<const bf16_t *>(kv.data);
+    for (int i = 0; i < 3; ++i) {
+        a.qs[i] = qv.stride[i];
+        a.ks[i] = kv.stride[i];
+    }
+    a.v_descale = reinterpret_cast<const float *>(vd.data);
+    a.c = static_cast<float>(static_cast<float>(sc) * kLog2e);
+    return launch_fp8<false>(as_stream(stream), a);
+}
+
+}  // extern "C"

@@ -14,8 +14,9 @@ Numerics (tools/h3_attention.py:25-101):
     the last key tile is masked, so the three coincide.
 Only head_dim 128 (the DiT's) is built; D = 72 (Qwen vision) is not.
 
-fp8: `make_attention_fp8` / `quantize_fp8_per_head` add an OCP e4m3fn variant
-with per-head descales (no counterpart in the reference).
+fp8 (no counterpart in the reference): `quantize_fp8_per_head` (per-head
+absmax e4m3fn codes), `make_attention_fp8` (Q K^T and P.V on the fp8 MFMA)
+and `make_attention_fp8pv` (bf16 logits, fp8 P.V).
 """
 from __future__ import annotations
 
@@ -23,7 +24,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["make_attention", "make_attention_fp8", "quantize_fp8_per_head", "NUMERICS"]
+__all__ = ["make_attention", "make_attention_fp8", "make_attention_fp8pv", "quantize_fp8_per_head", "NUMERICS"]
 
 NUMERICS = ("fp32_qk", "fp32_qk_dotacc", "fp32_qk_split")
 
@@ -60,44 +61,76 @@ def make_attention(block_m=128, block_n=32, num_warps=4, num_stages=1, caller="t
     return kernel
 
 
-def quantize_fp8_per_head(x: torch.Tensor, x8: torch.Tensor | None = None,
+def quantize_fp8_per_head(x: torch.Tensor, transposed: bool = False, x8: torch.Tensor | None = None,
                           descale: torch.Tensor | None = None):
     """Per-head absmax e4m3fn quantisation of x [B, H, S, 128] (bf16).
-    Returns (x8 as torch.float8_e4m3fn [B, H, S, 128], descale fp32 [H]) with
-    x ~= x8 * descale[h]; descale = amax_h / 448."""
+    Returns (x8, descale): x8 a torch.float8_e4m3fn [B, H, S, 128] view and
+    descale fp32 [H] with x ~= x8 * descale[h], descale = amax_h / 448.
+    transposed=True stores x8 S-contiguous (physically [B, H, 128, S'] with S'
+    rounded up to 16), the layout the fp8 attention kernels read V in."""
     if x.dim() != 4:
         raise ValueError("x must be [B, H, S, D]")
     device = _lib.check_cuda(x)
     _lib.check_dtype(torch.bfloat16, x)
+    B, H, S, D = x.shape
     if x8 is None:
-        x8 = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=device)
+        if transposed:
+            s_pad = -(-S // 16) * 16
+            store = torch.empty(B, H, D, s_pad, dtype=torch.float8_e4m3fn, device=device)
+            x8 = store[..., :S].transpose(2, 3)
+        else:
+            x8 = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=device)
     if descale is None:
-        descale = torch.empty(x.shape[1], dtype=torch.float32, device=device)
+        descale = torch.empty(H, dtype=torch.float32, device=device)
     _lib.check_dtype(torch.float8_e4m3fn, x8)
     _lib.check_dtype(torch.float32, descale)
-    if x8.shape != x.shape or descale.shape != (x.shape[1],) or not descale.is_contiguous():
+    if x8.shape != x.shape or descale.shape != (H,) or not descale.is_contiguous():
         raise ValueError("x8 must match x and descale must be a contiguous [H] tensor")
     _lib.launch("launch_h3_quantize_fp8_per_head", device, _lib.tensor(x), _lib.tensor(x8.view(torch.uint8)),
                 _lib.tensor(descale))
     return x8, descale
 
 
+def _check_descales(h, *ds):
+    for d in ds:
+        _lib.check_dtype(torch.float32, d)
+        if d.shape != (h,) or not d.is_contiguous():
+            raise ValueError("descales must be contiguous fp32 [H] tensors")
+
+
 def make_attention_fp8():
-    """fp8 (e4m3fn) attention with per-head descales.
-    Returns kernel(q8, k8, v8, q_descale, k_descale, v_descale, scale, out)."""
+    """All-fp8 attention (e4m3fn Q, K, V, per-head descales, P requantised to
+    e4m3 per 64-key tile). v8 must be S-contiguous (quantize_fp8_per_head(v,
+    transposed=True)). Returns kernel(q8, k8, v8, q_descale, k_descale,
+    v_descale, scale, out) with out bf16 [B, H, Sq, 128]."""
 
     def kernel(q8, k8, v8, q_descale, k_descale, v_descale, scale, out):
         _check_qkvo(q8, k8, v8, out)
         device = _lib.check_cuda(q8, k8, v8, q_descale, k_descale, v_descale, out)
         _lib.check_dtype(torch.float8_e4m3fn, q8, k8, v8)
-        _lib.check_dtype(torch.float32, q_descale, k_descale, v_descale)
         _lib.check_dtype(torch.bfloat16, out)
-        for d in (q_descale, k_descale, v_descale):
-            if d.shape != (q8.shape[1],) or not d.is_contiguous():
-                raise ValueError("descales must be contiguous [H] tensors")
+        _check_descales(q8.shape[1], q_descale, k_descale, v_descale)
         _lib.launch("launch_h3_full_attention_fp8", device, _lib.tensor(q8.view(torch.uint8)),
                     _lib.tensor(k8.view(torch.uint8)), _lib.tensor(v8.view(torch.uint8)),
                     _lib.tensor(q_descale), _lib.tensor(k_descale), _lib.tensor(v_descale),
                     _lib.scalar(scale), _lib.tensor(out))
+
+    return kernel
+
+
+def make_attention_fp8pv():
+    """bf16 logits with an fp8 P.V product: q, k bf16 as for make_attention;
+    v8 e4m3fn S-contiguous with v_descale. Returns kernel(q, k, v8, v_descale,
+    scale, out)."""
+
+    def kernel(q, k, v8, v_descale, scale, out):
+        _check_qkvo(q, k, v8, out)
+        device = _lib.check_cuda(q, k, v8, v_descale, out)
+        _lib.check_dtype(torch.bfloat16, q, k, out)
+        _lib.check_dtype(torch.float8_e4m3fn, v8)
+        _check_descales(q.shape[1], v_descale)
+        _lib.launch("launch_h3_full_attention_fp8pv", device, _lib.tensor(q), _lib.tensor(k),
+                    _lib.tensor(v8.view(torch.uint8)), _lib.tensor(v_descale), _lib.scalar(scale),
+                    _lib.tensor(out))
 
     return kernel

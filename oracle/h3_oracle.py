@@ -37,8 +37,10 @@ How each function is pinned (tests/test_oracle.py):
   attention                 float64 brute force on tiny shapes, torch SDPA,
                             invariants (key permutation, constant V, identical
                             keys -> mean V, Sk = 1, dominant key, scale 0)
-  attention_fp8_emulated    fp32 attention within relative RMS 5e-2 (only pin:
-                            the reference has no fp8 path -- parity partial)
+  attention_fp8_emulated    fp32 attention: bf16 logits + fp8 P.V within
+                            relative RMS 5e-2 on outlier data; the all-fp8
+                            recipe within 5e-2 without outliers (no reference
+                            fp8 path exists -- parity partial)
 """
 from __future__ import annotations
 
@@ -269,15 +271,20 @@ def quantize_fp8_per_head(x: torch.Tensor):
     return codes, descale
 
 
-def attention_fp8_emulated(q8, k8, v8, q_descale, k_descale, v_descale, scale: float, block_n: int = 64):
-    """The fp8 algorithm on the CPU: fp32 logits from e4m3 codes times
-    q_descale*k_descale*scale, exp2 online softmax over `block_n`-key tiles, P
-    requantised per tile to e4m3 with the fixed factor 448, fp32 P.V, output
+def attention_fp8_emulated(q, k, v8, q_descale, k_descale, v_descale, scale: float, block_n: int = 64):
+    """The fp8 attention algorithm on the CPU. q, k: either e4m3 codes with
+    their per-head descales (the all-fp8 recipe) or bf16 tensors with
+    q_descale = k_descale = None (bf16 logits); v8: e4m3 codes. fp32 logits
+    times q_descale*k_descale*scale*log2(e), exact running max, exp2 online
+    softmax over `block_n`-key tiles, P requantised per tile to e4m3 with the
+    fixed factor 448, fp32 P.V and denominator (of the unquantised P), output
     acc * v_descale / (448 * denominator) in bf16. [B, H, S, D]."""
-    B, H, Sq, D = q8.shape
-    Sk = k8.shape[2]
-    qf, kf, vf = q8.float(), k8.float(), v8.float()
-    c = (q_descale * k_descale).view(1, H, 1, 1) * (scale * 1.4426950408889634)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    qf, kf, vf = q.float(), k.float(), v8.float()
+    c = torch.full((1, H, 1, 1), scale * 1.4426950408889634)
+    if q_descale is not None:
+        c = c * (q_descale * k_descale).view(1, H, 1, 1)
     m = torch.full((B, H, Sq, 1), -math.inf)
     den = torch.zeros(B, H, Sq, 1)
     acc = torch.zeros(B, H, Sq, D)

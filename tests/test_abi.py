@@ -1,0 +1,187 @@
+"""The C ABI of libh3mi355x.so on the CPU: the library loads, exports exactly
+the entry points include/h3mi355x.h declares, and every launcher rejects
+malformed arguments with hipErrorInvalidValue (1) on the host, before any HIP
+call -- so these run without a GPU. Empty launches return 0 without touching
+the device (patches/ninetoothed.patch:304-307)."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "h3mi355x.h"
+INVALID = 1
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._lib
+
+
+def declared_entry_points():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"NineToothedResult\s+(launch_\w+)\s*\(", text)))
+
+
+def declared_arity():
+    text = HEADER.read_text()
+    out = {}
+    for name, args in re.findall(r"NineToothedResult\s+(launch_\w+)\s*\(([^;]*)\);", text, re.S):
+        out[name] = args.count("NineToothedTensor")
+    return out
+
+
+def test_header_declares_the_binding_table(lib):
+    assert declared_entry_points() == sorted(lib.ENTRY_POINTS)
+    assert declared_arity() == lib.ENTRY_POINTS
+
+
+def test_library_exports_every_declared_symbol(lib):
+    so = lib.library()
+    for name in declared_entry_points():
+        assert hasattr(so, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(lib.LIBRARY_PATH)], capture_output=True, text=True)
+    exported = set(re.findall(r" T (launch_\w+)", nm.stdout))
+    assert exported == set(declared_entry_points())
+
+
+def test_library_is_built_for_gfx950(lib):
+    data = lib.LIBRARY_PATH.read_bytes()
+    assert b"gfx950" in data
+
+
+# ------------------------------------------------------------------ argument validation
+
+BUF = ctypes.create_string_buffer(1 << 16)
+ADDR = (ctypes.addressof(BUF) + 255) & ~255  # 256-byte aligned host memory, never dereferenced
+
+
+def t(shape, strides=None, data=ADDR):
+    if strides is None:
+        strides = []
+        acc = 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    return lambda L: L.raw_tensor(data, shape, strides)
+
+
+def scal(v=1e-6):
+    return lambda L: L.scalar(v)
+
+
+NULLSHAPE = lambda L: L._Arg(ADDR, (), None)  # noqa: E731  (tensor with NULL shape/strides)
+NULLSCALAR = lambda L: L._Arg(0, (), None)  # noqa: E731  (scalar with NULL data)
+
+CASES = [
+    # (entry point, args, why)
+    ("launch_h3_rms_exact_128", [t([1, 4, 64]), t([64]), scal(), t([1, 4, 64])], "width 64 on the 128 kernel"),
+    ("launch_h3_rms_exact_5376", [t([1, 4, 128]), t([128]), scal(), t([1, 4, 128])], "width 128 on the 5376 kernel"),
+    ("launch_h3_rms_exact", [t([1, 4, 128]), t([64]), scal(), t([1, 4, 128])], "weight length"),
+    ("launch_h3_rms_exact", [t([1, 4, 128]), t([128]), scal(), t([1, 5, 128])], "out shape"),
+    ("launch_h3_rms_exact", [t([1, 4, 128]), t([128]), NULLSCALAR, t([1, 4, 128])], "eps without data"),
+    ("launch_h3_rms_exact", [NULLSHAPE, t([128]), scal(), t([1, 4, 128])], "x without shape"),
+    ("launch_h3_rms_exact", [t([1, 2, 40000]), t([40000]), scal(), t([1, 2, 40000])], "width above 32768"),
+    ("launch_h3_rms_exact", [t([1, 4, 128], data=0), t([128]), scal(), t([1, 4, 128])], "null data"),
+    ("launch_h3_rms_modulate_exact", [t([1, 4, 128]), t([128]), scal(), t([1, 4, 64]), t([1, 4, 128]),
+                                      t([1, 4, 128])], "scale shape"),
+    ("launch_h3_gated_residual_exact", [t([1, 4, 128]), t([1, 4, 128]), t([1, 3, 128]), t([1, 4, 128])], "y shape"),
+    ("launch_h3_gated_residual_rms_modulate_exact",
+     [t([1, 4, 128]), t([1, 4, 128]), t([1, 4, 128]), t([128]), scal(), t([1, 4, 128]), t([1, 4, 128]),
+      t([1, 4, 127]), t([1, 4, 128])], "residual shape"),
+    ("launch_h3_swiglu_exact", [t([1, 4, 128]), t([1, 4, 256]), t([1, 4, 128])], "gate shape"),
+    ("launch_h3_rope_exact", [t([4, 2, 128]), t([4, 2, 128], data=ADDR + 256), t([4, 2, 128]), t([4, 48]),
+                              t([4, 48]), t([4, 2, 128]), t([4, 2, 128]), t([4, 2, 128])], "unaliased x views"),
+    ("launch_h3_rope_exact", [t([4, 2, 128])] * 3 + [t([4, 64]), t([4, 64])] + [t([4, 2, 128])] * 3, "table 64"),
+    ("launch_h3_rope_exact", [t([4, 2, 64])] * 3 + [t([4, 48]), t([4, 48])] + [t([4, 2, 64])] * 3, "head dim 64"),
+    ("launch_h3_qk_norm_rope", [t([4, 1, 2, 128])] * 3 + [t([128])] * 3 + [scal(), t([5, 48]), t([5, 48])]
+     + [t([4, 1, 2, 128])] * 3, "table rows != tokens"),
+    ("launch_h3_qk_norm_rope", [t([4, 1, 2, 128])] * 3 + [t([64])] * 3 + [scal(), t([4, 48]), t([4, 48])]
+     + [t([4, 1, 2, 128])] * 3, "weight 64"),
+    ("launch_h3_qk_norm_rope_interleaved", [t([4, 1, 2, 128]), t([128]), scal(), t([4, 48]), t([4, 48]),
+                                            t([4, 1, 2, 128])], "interleaved needs a 64-wide table"),
+    ("launch_h3_rope_cache", [t([4, 3]), t([15]), t([4, 48]), t([4, 48])], "15 powers"),
+    ("launch_h3_rope_cache", [t([4, 2]), t([16]), t([4, 48]), t([4, 48])], "2 position axes"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 64]), t([1, 2, 8, 64]), t([1, 2, 8, 64]), scal(0.1),
+                                  t([1, 2, 8, 64])], "head dim 64"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 3, 8, 128]), t([1, 3, 8, 128]), scal(0.1),
+                                  t([1, 2, 8, 128])], "head count mismatch"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 9, 128]), t([1, 2, 8, 128]), scal(0.1),
+                                  t([1, 2, 8, 128])], "k/v length mismatch"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128], [2048, 1024, 128, 2]), t([1, 2, 8, 128]),
+                                  t([1, 2, 8, 128]), scal(0.1), t([1, 2, 8, 128])], "non-unit head-dim stride"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128], data=ADDR + 2), t([1, 2, 8, 128]), t([1, 2, 8, 128]),
+                                  scal(0.1), t([1, 2, 8, 128])], "misaligned q"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 0, 128]), t([1, 2, 0, 128]), scal(0.1),
+                                  t([1, 2, 8, 128])], "no keys"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 8, 128]), t([1, 2, 8, 128]), NULLSCALAR,
+                                  t([1, 2, 8, 128])], "scale without data"),
+    ("launch_h3_full_attention", [t([1 << 16, 1 << 12, 1 << 20, 128]), t([1 << 16, 1 << 12, 8, 128]),
+                                  t([1 << 16, 1 << 12, 8, 128]), scal(0.1), t([1 << 16, 1 << 12, 1 << 20, 128])],
+     "grid above 2^31"),
+]
+
+
+@pytest.mark.parametrize("name,args,why", CASES, ids=[c[2] for c in CASES])
+def test_invalid_arguments_rejected_on_host(lib, name, args, why):
+    status = lib.call(name, 0, *(a(lib) for a in args))
+    assert status == INVALID, f"{name}: {why}: status {status}"
+
+
+EMPTY = [
+    ("launch_h3_rms_exact", [t([1, 0, 128]), t([128]), scal(), t([1, 0, 128])]),
+    ("launch_h3_rms_modulate_exact", [t([0, 4, 128]), t([128]), scal(), t([0, 4, 128]), t([0, 4, 128]),
+                                      t([0, 4, 128])]),
+    ("launch_h3_gated_residual_exact", [t([1, 0, 64])] * 4),
+    ("launch_h3_swiglu_exact", [t([1, 4, 0])] * 3),
+    ("launch_h3_qk_norm_rope", [t([0, 1, 2, 128])] * 3 + [t([128])] * 3 + [scal(), t([0, 48]), t([0, 48])]
+     + [t([0, 1, 2, 128])] * 3),
+    ("launch_h3_rope_cache", [t([0, 3]), t([16]), t([0, 48]), t([0, 48])]),
+    ("launch_h3_full_attention", [t([1, 2, 0, 128]), t([1, 2, 8, 128]), t([1, 2, 8, 128]), scal(0.1),
+                                  t([1, 2, 0, 128])]),
+]
+
+
+@pytest.mark.parametrize("name,args", EMPTY, ids=[e[0] for e in EMPTY])
+def test_empty_launch_is_a_no_op(lib, name, args):
+    assert lib.call(name, 0, *(a(lib) for a in args)) == 0
+
+
+# ------------------------------------------------------------------ Python faces
+
+def test_python_factories_validate(pkg):
+    with pytest.raises(ValueError):
+        pkg.make_attention(head_dim=64)
+    with pytest.raises(ValueError):
+        pkg.make_attention(head_dim=0)
+    with pytest.raises(ValueError):
+        pkg.make_attention(numerics="tf32")
+    with pytest.raises(ValueError):
+        pkg.make_attention(dtype=torch.float16)
+    with pytest.raises(ValueError):
+        pkg.make_qk_norm_rope(block_tokens=2, ranks=2)
+    with pytest.raises(ValueError):
+        pkg.make_swiglu(dtype="float16")
+    for numerics in ("fp32_qk", "fp32_qk_dotacc", "fp32_qk_split"):
+        assert callable(pkg.make_attention(numerics=numerics))
+
+
+def test_python_faces_reject_host_tensors(pkg):
+    x = torch.zeros(1, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="cuda"):
+        pkg.make_rms(width=128)(x, torch.zeros(128, dtype=torch.bfloat16), 1e-6, x)
+    q = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        pkg.make_attention()(q, q, q, 0.1, q)
+    with pytest.raises(ValueError):
+        pkg.make_attention()(q[0], q, q, 0.1, q)
+
+
+def test_raw_qk_norm_rope_form_is_twelve_arguments(pkg):
+    raw = pkg.make_qk_norm_rope(caller="hip")
+    assert raw.__code__.co_argcount == 12

@@ -1,0 +1,453 @@
+"""Pins the CPU oracle (oracle/h3_oracle.py) without trusting its own formulas:
+closed forms, float64 evaluations, brute force on tiny inputs, invariants, and
+an exhaustive sweep where the input space is small. Each check is chosen so a
+plausible mistake (a dropped rounding step, the wrong RoPE pairing, a
+transposed operand, a missing weight) fails it. CPU only."""
+from __future__ import annotations
+
+import itertools
+import math
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import h3_oracle as o
+
+BF = torch.bfloat16
+
+
+def all_bf16(finite_only=True):
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(BF)
+    if finite_only:
+        x = x[torch.isfinite(x.float())]
+    return x
+
+
+def bf16_round_f64(x: torch.Tensor) -> torch.Tensor:
+    """float64 -> bf16 with one rounding (no detour through fp32)."""
+    # Round-to-nearest-even on the 64-bit pattern to 8 significant bits.
+    x = x.double()
+    m, e = torch.frexp(x)  # x = m * 2^e, 0.5 <= |m| < 1
+    scaled = torch.ldexp(m, torch.full_like(e, 8))
+    r = torch.round(scaled)  # round half to even
+    return torch.ldexp(r / 256.0, e).float().to(BF)
+
+
+def near_bf16_midpoint(x64: torch.Tensor, rel=2.0 ** -22) -> torch.Tensor:
+    """True where a float64 value lies so close to a bf16 rounding midpoint that
+    rounding through fp32 first may flip the result."""
+    m, e = torch.frexp(x64.double())
+    frac = torch.ldexp(m.abs(), torch.full_like(e, 8))
+    return (frac - frac.floor() - 0.5).abs() < rel * 256
+
+
+# ------------------------------------------------------------------ rounding helpers
+
+def test_bf16_round_helper_matches_torch_on_exact_fp32():
+    x = torch.randn(10000, dtype=torch.float32)
+    assert torch.equal(bf16_round_f64(x.double()), x.to(BF))
+
+
+def test_ulp_distance():
+    a = torch.tensor([1.0, 1.0, -1.0, 0.0, 0.0], dtype=BF)
+    b = torch.tensor([1.0078125, 1.0, -1.0078125, -0.0, 2.0 ** -133], dtype=BF)
+    assert o.ulp_distance(a, b).tolist() == [1, 0, 1, 0, 1]
+    assert int(o.ulp_distance(torch.tensor([float("nan")], dtype=BF), torch.tensor([float("nan")], dtype=BF))) == 0
+
+
+# ------------------------------------------------------------------ fixed-order sum
+
+def _py_fixed_sum(row):
+    """Pure-Python statement of the documented order, fp32 via struct."""
+    f32 = lambda v: struct.unpack("f", struct.pack("f", v))[0]  # noqa: E731
+    W = len(row)
+    groups = -(-W // 8)
+    threads = 1
+    if groups <= 64:
+        while threads < groups:
+            threads *= 2
+    else:
+        threads = 256
+    partial = [0.0] * threads
+    for t in range(threads):
+        g = t
+        while g < groups:
+            for e in range(8):
+                idx = 8 * g + e
+                if idx < W:
+                    partial[t] = f32(partial[t] + row[idx])
+            g += threads
+    lanes = min(threads, 64)
+    waves = [partial[w * lanes:(w + 1) * lanes] for w in range(threads // lanes)]
+    folded = []
+    for p in waves:
+        n = lanes
+        while n > 1:
+            n //= 2
+            p = [f32(p[i] + p[i + n]) for i in range(n)]
+        folded.append(p[0])
+    n = len(folded)
+    while n > 1:
+        n //= 2
+        folded = [f32(folded[i] + folded[i + n]) for i in range(n)]
+    return folded[0]
+
+
+@pytest.mark.parametrize("W", [1, 7, 8, 20, 100, 128, 512, 600, 1000, 5376])
+def test_fixed_order_sum_matches_python_statement(W):
+    gen = torch.Generator().manual_seed(W)
+    x = torch.rand(3, W, generator=gen) * torch.exp2(torch.randint(-20, 20, (3, W), generator=gen).float())
+    got = o.fixed_order_sum(x)
+    for r in range(3):
+        assert float(got[r]) == _py_fixed_sum([float(v) for v in x[r]])
+
+
+def test_fixed_order_sum_error_bound():
+    x = torch.rand(64, 7168) * 4
+    got = o.fixed_order_sum(x).double()
+    exact = x.double().sum(-1)
+    bound = 7168 * 2.0 ** -24 * x.double().abs().sum(-1)
+    assert bool(((got - exact).abs() <= bound).all())
+
+
+# ------------------------------------------------------------------ SwiGLU
+
+def test_swiglu_exhaustive_against_float64():
+    g = all_bf16()
+    up = torch.ones_like(g)
+    got = o.swiglu(up, g)
+    g64 = g.double()
+    e64 = torch.exp(-g64)
+    # exp(-g) is an fp32 intermediate in the reference: it overflows to +inf
+    # below g = -88.72, where g / (1 + inf) = -0.
+    e64 = torch.where(e64 > torch.finfo(torch.float32).max, torch.full_like(e64, float("inf")), e64)
+    act64 = g64 / (1.0 + e64)
+    ref = bf16_round_f64(act64)
+    diff = o.ulp_distance(got, ref)
+    # Every disagreement must sit at a bf16 rounding midpoint (fp32 steps).
+    assert bool((near_bf16_midpoint(act64)[diff > 0]).all())
+    assert int(diff.max()) <= 1
+    # SiLU written another way (x * sigmoid(x)) agrees within 1 ulp.
+    silu = torch.nn.functional.silu(g.float()).to(BF)
+    assert int(o.ulp_distance(got, silu).max()) <= 1
+
+
+@pytest.mark.parametrize("u", [1.0, -1.0, 0.125, 3.0, 0.0])
+def test_swiglu_up_scaling(u):
+    g = all_bf16()
+    base = o.swiglu(torch.ones_like(g), g)
+    got = o.swiglu(torch.full_like(g, u), g)
+    # up * act with act already bf16: one fp32 product, one rounding.
+    assert torch.equal(got.float(), (base.float() * u).to(BF).float()) or u == 3.0
+    if u == 3.0:
+        ref = bf16_round_f64(base.double() * 3.0)
+        assert torch.equal(got, ref)
+
+
+def test_swiglu_special_values():
+    g = torch.tensor([float("inf"), float("-inf"), float("nan"), 0.0, -0.0], dtype=BF)
+    out = o.swiglu(torch.ones_like(g), g).float()
+    assert out[0] == float("inf") and math.isnan(out[1]) and math.isnan(out[2]) and out[3] == 0 and out[4] == 0
+
+
+# ------------------------------------------------------------------ gated residual
+
+def test_gated_residual_closed_forms():
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(64, 300, generator=gen).to(BF)
+    y = torch.randn(64, 300, generator=gen).to(BF)
+    one, zero = torch.ones_like(x), torch.zeros_like(x)
+    assert torch.equal(o.gated_residual(x, one, y), (x.float() + y.float()).to(BF))
+    assert torch.equal(o.gated_residual(x, zero, y), x)
+    assert bool((o.gated_residual(x, -one, x).float() == 0).all())
+
+
+def test_gated_residual_against_float64():
+    gen = torch.Generator().manual_seed(2)
+    x = (torch.randn(200, 512, generator=gen) * 8).to(BF)
+    y = torch.randn(200, 512, generator=gen).to(BF)
+    g = (torch.randn(200, 512, generator=gen) * 0.5).to(BF)
+    got = o.gated_residual(x, g, y)
+    product = bf16_round_f64(g.double() * y.double())  # exact in fp32 already
+    s64 = x.double() + product.double()
+    ref = bf16_round_f64(s64)
+    diff = o.ulp_distance(got, ref)
+    assert bool(near_bf16_midpoint(s64)[diff > 0].all())
+    # The product must be rounded to bf16 before the sum: skipping that step
+    # changes many elements.
+    unrounded = bf16_round_f64(x.double() + g.double() * y.double())
+    assert int((o.ulp_distance(got, unrounded) > 0).sum()) > 100
+
+
+# ------------------------------------------------------------------ RMS family
+
+def test_rms_constant_rows_closed_form():
+    W = 5376
+    w = (1 + 0.1 * torch.randn(W)).to(BF)
+    for c in (1.0, 2.0, 0.375, 3.0, 100.0):
+        x = torch.full((2, 3, W), c, dtype=BF)
+        got = o.rms_norm(x, w, 1e-6)
+        sq = torch.tensor(c * c, dtype=torch.float32).to(BF).float()
+        var = (sq + torch.tensor(1e-6, dtype=torch.float32).to(BF).float()).to(BF).float()
+        r = (1.0 / torch.sqrt(var)).to(BF).float()
+        n = (torch.tensor(c) * r).to(BF).float()
+        ref = (n * w.float()).to(BF)
+        assert torch.equal(got, ref.expand_as(got))
+
+
+def test_rms_zero_rows_and_eps():
+    w = torch.randn(128).to(BF)
+    x = torch.zeros(4, 1, 128, dtype=BF)
+    assert bool((o.rms_norm(x, w, 1e-6).float() == 0).all())
+    # Tiny rows: eps dominates; bf16-rounded eps (kernel) vs fp32 eps (eager).
+    x = torch.full((1, 1, 128), 1e-4, dtype=BF)
+    a = o.rms_norm(x, w, 1e-6, eps_rounding="bf16")
+    b = o.rms_norm(x, w, 1e-6, eps_rounding="fp32")
+    assert a.shape == b.shape
+
+
+@pytest.mark.parametrize("W", [128, 5376, 7168])
+def test_rms_power_of_two_scale_invariance(W):
+    gen = torch.Generator().manual_seed(W)
+    x = torch.randn(8, 16, W, generator=gen).to(BF)
+    w = torch.randn(W, generator=gen).to(BF)
+    base = o.rms_norm(x, w, 1e-6)
+    for k in (-3, 2, 5):
+        assert torch.equal(o.rms_norm((x.float() * 2.0 ** k).to(BF), w, 1e-6), base)
+
+
+@pytest.mark.parametrize("W", [128, 5376])
+def test_rms_against_float64(W):
+    gen = torch.Generator().manual_seed(7)
+    x = (torch.randn(16, 32, W, generator=gen) * 3).to(BF)
+    w = (1 + 0.1 * torch.randn(W, generator=gen)).to(BF)
+    got = o.rms_norm(x, w, 1e-6).double()
+    x64 = x.double()
+    ref = x64 / torch.sqrt((x64 * x64).mean(-1, keepdim=True) + 1e-6) * w.double()
+    rel = (got - ref).abs() / ref.abs().clamp_min(1e-3)
+    assert float(rel.max()) < 2.0 ** -5  # a few bf16 ulps of staged rounding
+    assert float(rel.mean()) < 2.0 ** -8
+    # Omitting the weight or dividing by W-1 is caught.
+    assert float(((x64 / torch.sqrt((x64 * x64).mean(-1, keepdim=True))) - got).abs().max()) > 0.01
+
+
+def test_rms_fixed_vs_torch_order_ties_only():
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(2048, 7168, generator=gen).to(BF)
+    w = torch.randn(7168, generator=gen).to(BF)
+    a = o.rms_norm(x, w, 1e-6, order="fixed")
+    b = o.rms_norm(x, w, 1e-6, order="torch")
+    v = x.float()
+    sq = o.rb(v * v)
+    ties = o.rb(o.fixed_order_sum(sq) / 7168) != o.rb(sq.sum(-1) / 7168)
+    d = o.ulp_distance(a, b)
+    assert int(d[~ties].max()) == 0
+    assert int(ties.sum()) < 20
+
+
+def test_modulate_closed_forms():
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(4, 8, 512, generator=gen).to(BF)
+    w = torch.randn(512, generator=gen).to(BF)
+    shift = torch.randn(4, 8, 512, generator=gen).to(BF)
+    minus_one = torch.full_like(x, -1.0)
+    zero = torch.zeros_like(x)
+    # scale = -1: factor 0, out = shift (the AdaLN edge of tools/verify_h3_pointwise_native.py:118).
+    assert torch.equal(o.rms_modulate(x, w, 1e-6, minus_one, shift), (shift.float() + 0.0).to(BF))
+    assert torch.equal(o.rms_modulate(x, w, 1e-6, zero, zero), o.rms_norm(x, w, 1e-6))
+
+
+def test_gated_residual_rms_modulate_gate_zero():
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 16, 256, generator=gen).to(BF)
+    y = torch.randn(2, 16, 256, generator=gen).to(BF)
+    w = torch.randn(256, generator=gen).to(BF)
+    sc = torch.randn(2, 16, 256, generator=gen).to(BF)
+    sh = torch.randn(2, 16, 256, generator=gen).to(BF)
+    res, out = o.gated_residual_rms_modulate(x, torch.zeros_like(x), y, w, 1e-6, sc, sh)
+    assert torch.equal(res, x)
+    assert torch.equal(out, o.rms_modulate(x, w, 1e-6, sc, sh))
+
+
+# ------------------------------------------------------------------ RoPE
+
+def test_rope_rotate_half_identity_and_quarter_turn():
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(10, 3, 128, generator=gen).to(BF)
+    one, zero = torch.ones(10, 1, 48, dtype=BF), torch.zeros(10, 1, 48, dtype=BF)
+    assert torch.equal(o.rope_rotate_half(x, one, zero), x)
+    y = o.rope_rotate_half(x, zero, one)
+    assert torch.equal(y[..., :48], -x[..., 48:96])
+    assert torch.equal(y[..., 48:96], x[..., :48])
+    assert torch.equal(y[..., 96:], x[..., 96:])
+
+
+def test_rope_interleaved_identity_and_quarter_turn():
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(10, 3, 128, generator=gen).to(BF)
+    one, zero = torch.ones(10, 1, 64, dtype=BF), torch.zeros(10, 1, 64, dtype=BF)
+    assert torch.equal(o.rope_interleaved(x, one, zero), x)
+    y = o.rope_interleaved(x, zero, one)
+    assert torch.equal(y[..., 0::2], -x[..., 1::2])
+    assert torch.equal(y[..., 1::2], x[..., 0::2])
+
+
+@pytest.mark.parametrize("form", ["rotate_half", "interleaved"])
+def test_rope_preserves_pair_norms(form):
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(64, 4, 128, generator=gen).to(BF)
+    n = 48 if form == "rotate_half" else 64
+    theta = torch.rand(64, 1, n, generator=gen) * 6.28
+    c, s = theta.cos().to(BF), theta.sin().to(BF)
+    if form == "rotate_half":
+        y = o.rope_rotate_half(x, c, s).double()
+        px = x.double()[..., :48] ** 2 + x.double()[..., 48:96] ** 2
+        py = y[..., :48] ** 2 + y[..., 48:96] ** 2
+    else:
+        y = o.rope_interleaved(x, c, s).double()
+        px = x.double()[..., 0::2] ** 2 + x.double()[..., 1::2] ** 2
+        py = y[..., 0::2] ** 2 + y[..., 1::2] ** 2
+    rel = (py.sqrt() - px.sqrt()).abs() / px.sqrt().clamp_min(1e-2)
+    assert float(rel.max()) < 0.03
+
+
+def test_qk_norm_rope_is_norm_then_rope():
+    gen = torch.Generator().manual_seed(10)
+    x = torch.randn(33, 2, 3, 128, generator=gen).to(BF)
+    w = torch.randn(128, generator=gen).to(BF)
+    one, zero = torch.ones(33, 48, dtype=BF), torch.zeros(33, 48, dtype=BF)
+    assert torch.equal(o.qk_norm_rope(x, w, 1e-6, one, zero), o.rms_norm(x, w, 1e-6))
+    one64, zero64 = torch.ones(33, 64, dtype=BF), torch.zeros(33, 64, dtype=BF)
+    assert torch.equal(o.qk_norm_rope_interleaved(x, w, 1e-6, one64, zero64), o.rms_norm(x, w, 1e-6))
+
+
+# ------------------------------------------------------------------ RoPE tables
+
+def test_rope_powers_closed_form():
+    p = o.rope_powers().double()
+    ref = torch.tensor([10000.0 ** (k / 16) for k in range(16)], dtype=torch.float64)
+    assert float(((p - ref).abs() / ref).max()) < 2e-7
+
+
+@pytest.mark.parametrize("kind", ["grid", "integer", "fine"])
+def test_rope_cache_against_float64(kind):
+    if kind == "grid":
+        pos = o.grid_positions(8, 32, 32)
+    elif kind == "integer":
+        pos = torch.randint(0, 4096, (3000, 3), generator=torch.Generator().manual_seed(0)).double()
+    else:
+        pos = torch.arange(9000).double().view(-1, 3) / 37
+    power = o.rope_powers()
+    got = o.rope_cache(pos, power)
+    angle = (pos.float().unsqueeze(-1) * (1.0 / power).view(1, 1, -1)).flatten(1).double()
+    ref = torch.cat([bf16_round_f64(angle.cos()), bf16_round_f64(angle.sin())], dim=-1)
+    assert int(o.ulp_distance(got, ref).max()) <= 1
+    assert got.shape == (pos.shape[0], 96)
+    if kind == "grid":
+        assert torch.equal(got[0, :48].float(), torch.ones(48)) and torch.equal(got[0, 48:].float(), torch.zeros(48))
+
+
+def test_rope_table_interleaved_axes():
+    pos = o.grid_positions(8, 32, 32)
+    cos, sin = o.rope_table_interleaved(pos)
+    assert cos.shape == (8192, 64)
+    # Pair 0 of each axis rotates by the raw position (frequency 1).
+    for a, first in ((0, 0), (1, 16), (2, 40)):
+        ref = bf16_round_f64(pos[:, a].float().double().cos())
+        assert int(o.ulp_distance(cos[:, first], ref).max()) <= 1
+    # Last pair of axis h (j = 23 of 24): theta^(-46/48).
+    inv = 1.0 / (10000.0 ** (46 / 48))
+    ref = bf16_round_f64((pos[:, 1].float() * torch.tensor(inv, dtype=torch.float32)).double().sin())
+    assert int(o.ulp_distance(sin[:, 39], ref).max()) <= 1
+
+
+# ------------------------------------------------------------------ attention
+
+def _brute_attention(q, k, v, scale):
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    out = torch.zeros(B, H, Sq, v.shape[-1], dtype=torch.float64)
+    for b, h, i in itertools.product(range(B), range(H), range(Sq)):
+        logits = [scale * sum(float(q[b, h, i, d]) * float(k[b, h, j, d]) for d in range(D)) for j in range(Sk)]
+        mx = max(logits)
+        w = [math.exp(l - mx) for l in logits]
+        den = sum(w)
+        for e in range(v.shape[-1]):
+            out[b, h, i, e] = sum(w[j] * float(v[b, h, j, e]) for j in range(Sk)) / den
+    return out
+
+
+def test_attention_matches_brute_force():
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(1, 2, 3, 5, generator=gen).to(BF)
+    k = torch.randn(1, 2, 4, 5, generator=gen).to(BF)
+    v = torch.randn(1, 2, 4, 6, generator=gen).to(BF)
+    got = o.attention(q, k, v, 0.7)
+    assert torch.allclose(got, _brute_attention(q, k, v, 0.7), atol=1e-12)
+
+
+def test_attention_matches_torch_sdpa():
+    gen = torch.Generator().manual_seed(12)
+    q, k, v = (torch.randn(1, 3, 100, 128, generator=gen) for _ in range(3))
+    got = o.attention(q, k, v, 128 ** -0.5, dtype=torch.float32)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+    assert torch.allclose(got, ref, atol=1e-5)
+
+
+def test_attention_invariants():
+    gen = torch.Generator().manual_seed(13)
+    q = torch.randn(1, 1, 7, 16, generator=gen)
+    k = torch.randn(1, 1, 9, 16, generator=gen)
+    v = torch.randn(1, 1, 9, 16, generator=gen)
+    base = o.attention(q, k, v, 0.3)
+    perm = torch.randperm(9, generator=gen)
+    assert torch.allclose(o.attention(q, k[:, :, perm], v[:, :, perm], 0.3), base, atol=1e-12)
+    const_v = torch.ones_like(v) * 2.5
+    assert torch.allclose(o.attention(q, k, const_v, 0.3), torch.full_like(base, 2.5), atol=1e-12)
+    same_k = k[:, :, :1].expand_as(k)
+    assert torch.allclose(o.attention(q, same_k, v, 0.3), v.double().mean(2, keepdim=True).expand_as(base), atol=1e-12)
+    assert torch.allclose(o.attention(q, k, v, 0.0), v.double().mean(2, keepdim=True).expand_as(base), atol=1e-12)
+    assert torch.allclose(o.attention(q, k[:, :, :1], v[:, :, :1], 0.3), v[:, :, :1].double().expand_as(base))
+    dominant = k.clone()
+    dominant[:, :, 4] = q[:, :, 0] * 50
+    out = o.attention(q[:, :, :1], dominant, v, 1.0)
+    assert torch.allclose(out[0, 0, 0], v[0, 0, 4].double(), atol=1e-6)
+
+
+def test_fp8_quantisation():
+    q, _, _ = o.attention_inputs(512, H=2, seed=3, outlier_fraction=0.01)
+    x = q.transpose(1, 2)
+    x8, d = o.quantize_fp8_per_head(x)
+    amax = x.float().abs().amax(dim=(0, 2, 3))
+    assert torch.allclose(x8.float().abs().amax(dim=(0, 2, 3)), torch.full_like(amax, 448.0))
+    back = x8.float() * d.view(1, -1, 1, 1)
+    # e4m3: 3 mantissa bits -> relative half-ulp 2^-4 for normal values.
+    normal = x.float().abs() >= amax.view(1, -1, 1, 1) * 2.0 ** -6 / 448 * 64
+    rel = ((back - x.float()).abs() / x.float().abs())[normal]
+    assert float(rel.max()) <= 2.0 ** -4 + 1e-6
+
+
+def _fp8_case(S, outliers):
+    q, k, v = o.attention_inputs(S, H=2, seed=3, outlier_fraction=outliers)
+    q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    rows = torch.arange(0, S, 4)
+    ref = o.attention(q[:, :, rows], k, v, 128 ** -0.5)
+    q8, qd = o.quantize_fp8_per_head(q)
+    k8, kd = o.quantize_fp8_per_head(k)
+    v8, vd = o.quantize_fp8_per_head(v)
+    full = o.attention_fp8_emulated(q8[:, :, rows], k8, v8, qd, kd, vd, 128 ** -0.5)
+    mixed = o.attention_fp8_emulated(q[:, :, rows], k, v8, None, None, vd, 128 ** -0.5)
+    rel = lambda out: float((out.double() - ref).norm() / ref.norm())  # noqa: E731
+    return rel(full), rel(mixed)
+
+
+def test_fp8_emulated_attention_error_budget():
+    full, mixed = _fp8_case(2048, 0.0)
+    assert full <= 6e-2 and mixed <= 5e-2, (full, mixed)
+    full, mixed = _fp8_case(2048, 0.01)
+    # With 1% of key rows x8 the e4m3 logits err by ~5% of up to ~30 log2
+    # units: the all-fp8 recipe misses 5e-2, bf16 logits + fp8 P.V meet it.
+    assert mixed <= 5e-2 and full > mixed, (full, mixed)
