@@ -192,6 +192,10 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-pointwise", action="store_true")
     parser.add_argument("--no-extra", action="store_true", help="skip the S=8192 and fp8 attention lines")
+    parser.add_argument("--pointwise-only", action="store_true",
+                        help="time only the pointwise ops (for per-kernel profiles)")
+    parser.add_argument("--copy-calibration", type=int, metavar="MIB",
+                        help="run a plain device copy of MIB MiB five times (PMC byte-counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU's share (14 heads at full sequence length); runs on more than one "
@@ -205,6 +209,18 @@ def main() -> int:
     torch.cuda.set_device(device)
     props = torch.cuda.get_device_properties(device)
     log(f"device {props.name} ({props.gcnArchName}), torch {torch.__version__}")
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}))
+        return 0
+    if args.pointwise_only:
+        print(json.dumps({"pointwise": bench_pointwise(pkg, device)}))
+        return 0
 
     S, H, D = 73984, 14, 128
     q, k, v = attention_inputs_gpu(S, H, 0, 0.01, device)
@@ -230,9 +246,13 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
     }
-    profile = ROOT / "profiles" / "attention_s73984_traffic.json"
+    # HBM bytes per launch of this kernel, measured with FETCH_SIZE / WRITE_SIZE
+    # counters (calibrated on a plain copy) and recorded in the profile summary.
+    profile = ROOT / "profiles" / "attention_bf16_s73984_traffic.md"
     if profile.exists():
-        line["roofline"]["traffic"] = json.loads(profile.read_text()).get("hbm_bytes_per_launch")
+        for text_line in profile.read_text().splitlines():
+            if text_line.startswith("hbm_bytes_per_launch:"):
+                line["roofline"]["traffic"] = int(text_line.split(":")[1].strip())
     del q, k, v, out
 
     if not args.no_extra:
@@ -246,6 +266,29 @@ def main() -> int:
                                    "frac": round(t2 / BF16_PEAK_TFLOPS, 4)}
         log(f"attention S={S2} H={H}: {ms2:.3f} ms, {t2:.1f} TFLOP/s")
         del q, k, v, out
+
+    if not args.no_extra:
+        # fp8 configuration: the same S = 73,984 tensors, per-head e4m3fn.
+        q, k, v = attention_inputs_gpu(S, H, 0, 0.01, device)
+        qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        out = torch.empty_like(q)
+        quant = lambda: (pkg.quantize_fp8_per_head(qt), pkg.quantize_fp8_per_head(kt),  # noqa: E731
+                         pkg.quantize_fp8_per_head(vt, transposed=True))
+        ms_q = time_launches(quant, 5, 1)
+        (q8, qd), (k8, kd), (v8, vd) = quant()
+        f8 = pkg.make_attention_fp8()
+        f8pv = pkg.make_attention_fp8pv()
+        ms_f8 = time_launches(lambda: f8(q8, k8, v8, qd, kd, vd, scale, out.transpose(1, 2)), args.steps, 2)
+        ms_pv = time_launches(lambda: f8pv(qt, kt, v8, vd, scale, out.transpose(1, 2)), args.steps, 2)
+        t8, tpv = flops / (ms_f8 * 1e-3) / 1e12, flops / (ms_pv * 1e-3) / 1e12
+        line["fp8"] = {
+            "all_fp8": {"ms": round(ms_f8, 4), "TFLOP/s": round(t8, 2), "frac_fp8_peak": round(t8 / FP8_PEAK_TFLOPS, 4)},
+            "fp8_pv_bf16_logits": {"ms": round(ms_pv, 4), "TFLOP/s": round(tpv, 2)},
+            "quantize_qkv_ms": round(ms_q, 4),
+        }
+        log(f"fp8 attention S={S}: all-fp8 {ms_f8:.3f} ms ({t8:.1f} TFLOP/s, {t8 / FP8_PEAK_TFLOPS:.1%} of fp8 peak); "
+            f"bf16 logits + fp8 P.V {ms_pv:.3f} ms ({tpv:.1f} TFLOP/s); quantise q,k,v {ms_q:.3f} ms")
+        del q, k, v, out, q8, k8, v8
 
     if not args.no_pointwise:
         log("pointwise ops:")
