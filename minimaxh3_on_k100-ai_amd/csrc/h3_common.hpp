@@ -129,6 +129,23 @@ __device__ __forceinline__ U4 ld16(const void *p) {
 __device__ __forceinline__ void st16(void *p, const U4 &v) {
     *static_cast<uint4 *>(p) = make_uint4(v.x, v.y, v.z, v.w);
 }
+// Non-temporal 16-byte accesses for data touched once (streamed rows): the
+// lines are not kept in the caches, leaving them to the reused operands.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ U4 ld16_stream(const void *p) {
+    const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t *>(p));
+    return {v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st16_stream(void *p, const U4 &v) {
+    const u32x4_t w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, static_cast<u32x4_t *>(p));
+}
+// Hides a packed group from the optimizer (an empty asm that may "change" its
+// registers), so values widened from it earlier are not kept alive in place of
+// widening it again: four packed registers instead of eight floats.
+__device__ __forceinline__ void keep_packed(U4 &v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
 __device__ __forceinline__ void u4_to_f8(const U4 &v, float f[8]) {
     f[0] = lo2f(v.x); f[1] = hi2f(v.x); f[2] = lo2f(v.y); f[3] = hi2f(v.y);
     f[4] = lo2f(v.z); f[5] = hi2f(v.z); f[6] = lo2f(v.w); f[7] = hi2f(v.w);

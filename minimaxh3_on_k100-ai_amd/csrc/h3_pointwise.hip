@@ -41,29 +41,54 @@ __device__ __forceinline__ bf16_t *row_ptr_w(const Rows &t, int64_t b, int64_t s
     return reinterpret_cast<bf16_t *>(t.p) + b * t.sb + s * t.ss;
 }
 
-// Loads the 8-element group starting at column c0 of a row: 16-byte vector on
-// the VEC path, element-wise (zero past W) otherwise.
-template <bool VEC>
-__device__ __forceinline__ void load8(const bf16_t *row, int64_t sw, int c0, int W, float f[8]) {
+// Loads the 8-element group starting at column c0 of a row as packed bf16: a
+// 16-byte vector on the VEC path (non-temporal when STREAM, for data read
+// once), element by element (zero past W) otherwise.
+template <bool VEC, bool STREAM = false>
+__device__ __forceinline__ U4 load_group(const bf16_t *row, int64_t sw, int c0, int W) {
     if constexpr (VEC) {
-        u4_to_f8(ld16(row + c0), f);
+        if constexpr (STREAM) {
+            return ld16_stream(row + c0);
+        } else {
+            return ld16(row + c0);
+        }
     } else {
+        // Element loads from clamped (valid) indices, zeroed past W by a select.
+        uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (c0 + e < W) ? bf2f(row[(c0 + e) * sw]) : 0.0f;
+        for (int e = 0; e < 8; e += 2) {
+            const int i0 = c0 + e < W ? c0 + e : W - 1, i1 = c0 + e + 1 < W ? c0 + e + 1 : W - 1;
+            const uint32_t lo = row[i0 * sw], hi = row[i1 * sw];
+            w[e / 2] = (c0 + e < W ? lo : 0u) | ((c0 + e + 1 < W ? hi : 0u) << 16);
+        }
+        return {w[0], w[1], w[2], w[3]};
     }
 }
 
-template <bool VEC>
-__device__ __forceinline__ void store8(bf16_t *row, int64_t sw, int c0, int W, const float f[8]) {
+template <bool VEC, bool STREAM = false>
+__device__ __forceinline__ void store_group(bf16_t *row, int64_t sw, int c0, int W, const U4 &v) {
     if constexpr (VEC) {
-        st16(row + c0, f8_to_u4(f));
+        if constexpr (STREAM) {
+            st16_stream(row + c0, v);
+        } else {
+            st16(row + c0, v);
+        }
     } else {
-        const U4 v = f8_to_u4(f);
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             if (c0 + e < W) row[(c0 + e) * sw] = static_cast<bf16_t>(w[e >> 1] >> (16 * (e & 1)));
     }
+}
+
+template <bool VEC, bool STREAM = false>
+__device__ __forceinline__ void load8(const bf16_t *row, int64_t sw, int c0, int W, float f[8]) {
+    u4_to_f8(load_group<VEC, STREAM>(row, sw, c0, W), f);
+}
+
+template <bool VEC, bool STREAM = false>
+__device__ __forceinline__ void store8(bf16_t *row, int64_t sw, int c0, int W, const float f[8]) {
+    store_group<VEC, STREAM>(row, sw, c0, W, f8_to_u4(f));
 }
 
 // Pairwise fold of one fp32 value over groups of L lanes (L a power of two <= 64).
@@ -85,12 +110,23 @@ struct RmsArgs {
     int64_t rows, S;
     int W;
     float eps_bf;  // eps already rounded fp64 -> fp32 -> bf16
+    bool staged;   // weight, scale, shift and gate are the same for every s of a batch entry
 };
 
+// bf16(1 + scale) of a group: the modulation factor, packed.
+__device__ __forceinline__ U4 factor_of(const U4 &scv) {
+    float sc[8];
+    u4_to_f8(scv, sc);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sc[e] += 1.0f;
+    return f8_to_u4(sc);
+}
+
 // The per-row epilogue shared by every path: value -> normalized -> weighted
-// (-> modulated). `r` is the bf16 reciprocal, widened.
+// (-> modulated). `r` is the bf16 reciprocal, widened; `k` the factor
+// bf16(1 + scale).
 template <int MODE>
-__device__ __forceinline__ void rms_epilogue(float f[8], float r, const float w[8], const float sc[8],
+__device__ __forceinline__ void rms_epilogue(float f[8], float r, const float w[8], const float k[8],
                                              const float sh[8]) {
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -102,9 +138,7 @@ __device__ __forceinline__ void rms_epilogue(float f[8], float r, const float w[
             f[e + 1] = a1;
         } else {
             rbf2(a0, a1);  // weighted = bf16(normalized * weight)
-            float k0 = 1.0f + sc[e], k1 = 1.0f + sc[e + 1];
-            rbf2(k0, k1);  // factor = bf16(1 + scale)
-            float p0 = a0 * k0, p1 = a1 * k1;
+            float p0 = a0 * k[e], p1 = a1 * k[e + 1];
             rbf2(p0, p1);  // product = bf16(weighted * factor)
             f[e] = p0 + sh[e];  // out = bf16(product + shift), rounded by the store
             f[e + 1] = p1 + sh[e + 1];
@@ -112,124 +146,448 @@ __device__ __forceinline__ void rms_epilogue(float f[8], float r, const float w[
     }
 }
 
-// One row per group of L lanes (L <= 64, one 8-element group per lane), or
-// one row per 256-thread block (L == 256, VPT groups per thread).
-template <int L, int VPT, bool VEC, int MODE>
-__global__ __launch_bounds__(kThreads) void rms_rows_kernel(RmsArgs a) {
-    constexpr int kRowsPerBlock = L >= kThreads ? 1 : kThreads / L;
-    const int lane = threadIdx.x % (L >= kThreads ? kThreads : L);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / (L >= kThreads ? kThreads : L);
-    const bool row_ok = row < a.rows;
-    const int64_t b = row_ok ? row / a.S : 0;
-    const int64_t s = row_ok ? row % a.S : 0;
-    const int W = a.W;
-    const int W8 = (W + 7) / 8;
+// Launch shape of rms_staged_kernel: waves per block and about how many blocks.
+constexpr int kStagedThreads = 512;
+constexpr int kStagedBlocks = 512;
 
-    float v[VPT][8];
-    float partial = 0.0f;
-    const bf16_t *xr = row_ptr(a.x, b, s);
+// Loads are issued for every lane from a valid address, and only the arithmetic
+// and the stores are guarded: a load under a per-lane branch is waited for
+// before the branch closes, which would serialize a wave's loads. Groups past
+// the row read its last group (already in flight for another lane) and rows
+// past the end read the last row.
+__device__ __forceinline__ int clamp_group(int g, int W8) { return g < W8 ? g : W8 - 1; }
+
+// Phase 1 of one group: from the raw x (and, gated, gate and y) groups to the
+// value the row is normalized from (gated: the residual bf16(x + bf16(gate y)),
+// which the caller stores). When `valid`, its squares are added to `partial`
+// left to right; otherwise `partial` is unchanged.
+template <int MODE>
+__device__ __forceinline__ U4 rms_phase1(const U4 &xv, const U4 &gv, const U4 &yv, bool valid, float &partial) {
+    float f[8];
+    u4_to_f8(xv, f);
+    U4 v = xv;
+    if constexpr (MODE == kGatedRmsModulate) {
+        float gt[8], yy[8];
+        u4_to_f8(gv, gt);
+        u4_to_f8(yv, yy);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int g = lane + j * (L >= kThreads ? kThreads : L);
-        const bool ok = row_ok && g < W8;
-        if (ok) {
-            load8<VEC>(xr, a.x.sw, g * 8, W, v[j]);
-            if constexpr (MODE == kGatedRmsModulate) {
-                float gt[8], yy[8];
-                load8<VEC>(row_ptr(a.gate, b, s), a.gate.sw, g * 8, W, gt);
-                load8<VEC>(row_ptr(a.y, b, s), a.y.sw, g * 8, W, yy);
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    float p0 = gt[e] * yy[e], p1 = gt[e + 1] * yy[e + 1];
-                    rbf2(p0, p1);  // product = bf16(gate * y)
-                    float h0 = v[j][e] + p0, h1 = v[j][e + 1] + p1;
-                    rbf2(h0, h1);  // residual = bf16(x + product)
-                    v[j][e] = h0;
-                    v[j][e + 1] = h1;
-                }
-                if constexpr (!VEC) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (g * 8 + e >= W) v[j][e] = 0.0f;
-                }
-                store8<VEC>(row_ptr_w(a.residual, b, s), a.residual.sw, g * 8, W, v[j]);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                float q0 = v[j][e] * v[j][e], q1 = v[j][e + 1] * v[j][e + 1];
-                rbf2(q0, q1);  // squared = bf16(value * value)
-                partial += q0;
-                partial += q1;
-            }
+        for (int e = 0; e < 8; e += 2) {
+            float p0 = gt[e] * yy[e], p1 = gt[e + 1] * yy[e + 1];
+            rbf2(p0, p1);  // product = bf16(gate * y)
+            float h0 = f[e] + p0, h1 = f[e + 1] + p1;
+            rbf2(h0, h1);  // residual = bf16(x + product)
+            f[e] = h0;
+            f[e + 1] = h1;
         }
+        v = f8_to_u4(f);  // exact: the values are bf16
     }
-
-    // Fold the partials in the fixed order.
-    float total;
-    if constexpr (L >= kThreads) {
-        __shared__ float red[kThreads / 64];
-        const float wsum = fold_lanes<64>(partial);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = wsum;
-        __syncthreads();
-        total = (red[0] + red[2]) + (red[1] + red[3]);
-    } else {
-        total = fold_lanes<L>(partial);
+    float sum = partial;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        float q0 = f[e] * f[e], q1 = f[e + 1] * f[e + 1];
+        rbf2(q0, q1);  // squared = bf16(value * value)
+        sum += q0;
+        sum += q1;
     }
-    if (!row_ok) return;
+    partial = valid ? sum : partial;
+    return v;
+}
 
+// bf16 reciprocal RMS of a row from its fp32 sum of squares.
+__device__ __forceinline__ float rms_reciprocal(float total, int W, float eps_bf) {
     const float mean = rbf(__fdiv_rn(total, static_cast<float>(W)));  // bf16(sum / W)
-    const float var = rbf(mean + a.eps_bf);                           // bf16(mean + eps)
-    const float r = rbf(rsqrt_ieee(var));                             // bf16(rsqrt(var))
+    const float var = rbf(mean + eps_bf);                             // bf16(mean + eps)
+    return rbf(rsqrt_ieee(var));                                      // bf16(rsqrt(var))
+}
 
-    bf16_t *outr = row_ptr_w(a.out, b, s);
+// Phase 2 of one group: normalize, weight, modulate (kv = bf16(1 + scale)).
+template <int MODE>
+__device__ __forceinline__ U4 rms_phase2(const U4 &v, float r, const U4 &wv, const U4 &kv, const U4 &shv) {
+    float f[8], w[8], k[8], sh[8];
+    u4_to_f8(v, f);
+    u4_to_f8(wv, w);
+    if constexpr (MODE != kRms) {
+        u4_to_f8(kv, k);
+        u4_to_f8(shv, sh);
+    }
+    rms_epilogue<MODE>(f, r, w, k, sh);
+    return f8_to_u4(f);
+}
+
+// Rows of W8 <= 64 groups: a group of L lanes per row (L = next power of two
+// >= W8, lane g owns group g) and R rows per lane group. Every load of the
+// block (x, gate, y, weight, scale, shift) is issued before the first store.
+template <int L, int R, bool VEC, int MODE>
+__global__ __launch_bounds__(kThreads) void rms_lanes_kernel(RmsArgs a) {
+    constexpr int kGroups = kThreads / L;
+    const int lane = threadIdx.x % L;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kGroups * R + threadIdx.x / L;
+    const int W8 = (a.W + 7) / 8;
+    const int c0 = clamp_group(lane, W8) * 8;
+    int64_t b[R], s[R];
+    bool ok[R];
+    U4 xv[R], gv[R], yv[R], scv[R], shv[R];
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int g = lane + j * (L >= kThreads ? kThreads : L);
-        if (g >= W8) continue;
-        float w[8], sc[8], sh[8];
-        if constexpr (VEC) {
-            u4_to_f8(ld16(a.w + g * 8), w);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) w[e] = (g * 8 + e < W) ? bf2f(a.w[(g * 8 + e) * a.w_stride]) : 0.0f;
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = base + r * kGroups;
+        ok[r] = row < a.rows && lane < W8;
+        const int64_t rr = row < a.rows ? row : a.rows - 1;
+        b[r] = rr / a.S;
+        s[r] = rr % a.S;
+        xv[r] = load_group<VEC, true>(row_ptr(a.x, b[r], s[r]), a.x.sw, c0, a.W);
+        if constexpr (MODE == kGatedRmsModulate) {
+            gv[r] = load_group<VEC>(row_ptr(a.gate, b[r], s[r]), a.gate.sw, c0, a.W);
+            yv[r] = load_group<VEC, true>(row_ptr(a.y, b[r], s[r]), a.y.sw, c0, a.W);
         }
         if constexpr (MODE != kRms) {
-            load8<VEC>(row_ptr(a.scale, b, s), a.scale.sw, g * 8, W, sc);
-            load8<VEC>(row_ptr(a.shift, b, s), a.shift.sw, g * 8, W, sh);
+            scv[r] = load_group<VEC>(row_ptr(a.scale, b[r], s[r]), a.scale.sw, c0, a.W);
+            shv[r] = load_group<VEC>(row_ptr(a.shift, b[r], s[r]), a.shift.sw, c0, a.W);
         }
-        rms_epilogue<MODE>(v[j], r, w, sc, sh);
-        store8<VEC>(outr, a.out.sw, g * 8, W, v[j]);
+    }
+    const U4 wv = load_group<VEC>(a.w, a.w_stride, c0, a.W);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float partial = 0.0f;
+        const U4 v = rms_phase1<MODE>(xv[r], gv[r], yv[r], ok[r], partial);
+        if constexpr (MODE == kGatedRmsModulate)
+            if (ok[r]) store_group<VEC, true>(row_ptr_w(a.residual, b[r], s[r]), a.residual.sw, c0, a.W, v);
+        const float rcp = rms_reciprocal(fold_lanes<L>(partial), a.W, a.eps_bf);
+        const U4 o = rms_phase2<MODE>(v, rcp, wv, factor_of(scv[r]), shv[r]);
+        if (ok[r]) store_group<VEC, true>(row_ptr_w(a.out, b[r], s[r]), a.out.sw, c0, a.W, o);
+    }
+}
+
+// Rows of 64 < W8 <= 64 * G groups with per-row modulation (or a generic
+// layout): one row per wave. Lane l takes groups l + 64k (k < G) and keeps four
+// partial sums, one for each of the threads l + 64w (w = k mod 4) of the
+// 256-thread order, which it reproduces exactly. Weight, scale and shift come
+// in batches of four groups, each batch's loads issued before the previous
+// batch's stores.
+template <int G, bool VEC, int MODE>
+__global__ __launch_bounds__(kThreads) void rms_wave_kernel(RmsArgs a) {
+    constexpr int kChunk = 4;
+    constexpr int kChunks = (G + kChunk - 1) / kChunk;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= a.rows) return;  // whole waves only; no block-level synchronization below
+    const int64_t b = row / a.S, s = row % a.S;
+    const int W8 = (a.W + 7) / 8;
+    U4 v[G], gv[G], yv[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int c0 = clamp_group(lane + 64 * k, W8) * 8;
+        v[k] = load_group<VEC, true>(row_ptr(a.x, b, s), a.x.sw, c0, a.W);
+        if constexpr (MODE == kGatedRmsModulate) {
+            gv[k] = load_group<VEC>(row_ptr(a.gate, b, s), a.gate.sw, c0, a.W);
+            yv[k] = load_group<VEC, true>(row_ptr(a.y, b, s), a.y.sw, c0, a.W);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
+    U4 wv[2][kChunk], scv[2][kChunk], shv[2][kChunk];
+    auto load_chunk = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const int c0 = clamp_group(lane + 64 * (c * kChunk + j), W8) * 8;
+            wv[c & 1][j] = load_group<VEC>(a.w, a.w_stride, c0, a.W);
+            if constexpr (MODE != kRms) {
+                scv[c & 1][j] = load_group<VEC>(row_ptr(a.scale, b, s), a.scale.sw, c0, a.W);
+                shv[c & 1][j] = load_group<VEC>(row_ptr(a.shift, b, s), a.shift.sw, c0, a.W);
+            }
+        }
+    };
+    load_chunk(0);
+    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int g = lane + 64 * k;
+        v[k] = rms_phase1<MODE>(v[k], gv[k], yv[k], g < W8, part[k & 3]);
+        if constexpr (MODE == kGatedRmsModulate)
+            if (g < W8) store_group<VEC, true>(row_ptr_w(a.residual, b, s), a.residual.sw, g * 8, a.W, v[k]);
+        keep_packed(v[k]);
+    }
+    const float total = (fold_lanes<64>(part[0]) + fold_lanes<64>(part[2])) +
+                        (fold_lanes<64>(part[1]) + fold_lanes<64>(part[3]));
+    const float r = rms_reciprocal(total, a.W, a.eps_bf);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        if (c + 1 < kChunks) load_chunk(c + 1);
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const int k = c * kChunk + j, g = lane + 64 * k;
+            if (k < G) {
+                const U4 o = rms_phase2<MODE>(v[k], r, wv[c & 1][j], factor_of(scv[c & 1][j]), shv[c & 1][j]);
+                if (g < W8) store_group<VEC, true>(row_ptr_w(a.out, b, s), a.out.sw, g * 8, a.W, o);
+            }
+        }
+    }
+}
+
+// Stages the row-invariant vectors of batch entry b in LDS: weight,
+// bf16(1 + scale), shift and (gated) gate, W8 groups each.
+template <int MODE, int THREADS>
+__device__ __forceinline__ void stage_vectors(const RmsArgs &a, int64_t b, int W8, U4 *staged) {
+    for (int g = threadIdx.x; g < W8; g += THREADS) {
+        staged[g] = ld16(a.w + g * 8);
+        if constexpr (MODE != kRms) {
+            staged[W8 + g] = factor_of(ld16(row_ptr(a.scale, b, 0) + g * 8));
+            staged[2 * W8 + g] = ld16(row_ptr(a.shift, b, 0) + g * 8);
+        }
+        if constexpr (MODE == kGatedRmsModulate) staged[3 * W8 + g] = ld16(row_ptr(a.gate, b, 0) + g * 8);
+    }
+    __syncthreads();
+}
+
+// Rows whose weight, modulation and gate vectors are the same for every s of
+// a batch entry b (broadcast over S, or S = 1), W8 <= 64 * G: the block stages
+// those vectors in LDS once, and each wave streams whole rows of b through
+// registers in the order of rms_wave_kernel, the rows grid-strided so that
+// the rows in flight are close together in memory. After a row's own loads the
+// only global accesses are its stores.
+template <int G, int MODE, int THREADS>
+__global__ __launch_bounds__(THREADS) void rms_staged_kernel(RmsArgs a) {
+    static_assert(MODE != kGatedRmsModulate, "the gated mode runs as rms_gated_pair_kernel");
+    extern __shared__ U4 staged[];
+    const int W8 = (a.W + 7) / 8;
+    const int64_t b = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * (THREADS / 64);
+    U4 v[G], yv[G];
+    auto load_row = [&](int64_t s) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int c0 = clamp_group(lane + 64 * k, W8) * 8;
+            v[k] = ld16_stream(row_ptr(a.x, b, s) + c0);
+            if constexpr (MODE == kGatedRmsModulate) yv[k] = ld16_stream(row_ptr(a.y, b, s) + c0);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
+    };
+    int64_t s = static_cast<int64_t>(blockIdx.x) * (THREADS / 64) + (threadIdx.x >> 6);
+    // The first row's loads go out before the vectors are staged.
+    if (s < a.S) load_row(s);
+    stage_vectors<MODE, THREADS>(a, b, W8, staged);
+    const U4 *lw = staged, *lk = staged + W8, *lsh = staged + 2 * W8, *lg = staged + 3 * W8;
+    for (bool first = true; s < a.S; s += step, first = false) {
+        if (!first) load_row(s);
+        float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int g = lane + 64 * k, gc = clamp_group(g, W8);
+            U4 gv{};
+            if constexpr (MODE == kGatedRmsModulate) gv = lg[gc];
+            v[k] = rms_phase1<MODE>(v[k], gv, yv[k], g < W8, part[k & 3]);
+            if constexpr (MODE == kGatedRmsModulate)
+                if (g < W8) st16_stream(row_ptr_w(a.residual, b, s) + g * 8, v[k]);
+            keep_packed(v[k]);
+        }
+        const float total = (fold_lanes<64>(part[0]) + fold_lanes<64>(part[2])) +
+                            (fold_lanes<64>(part[1]) + fold_lanes<64>(part[3]));
+        const float r = rms_reciprocal(total, a.W, a.eps_bf);
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int g = lane + 64 * k, gc = clamp_group(g, W8);
+            U4 kv{}, shv{};
+            if constexpr (MODE != kRms) {
+                kv = lk[gc];
+                shv = lsh[gc];
+            }
+            const U4 o = rms_phase2<MODE>(v[k], r, lw[gc], kv, shv);
+            if (g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+        }
+    }
+}
+
+// The gated mode of rms_staged_kernel with each row split over a pair of waves,
+// halving the registers that hold x and y: of the groups l + 64k, the first
+// wave takes those with k mod 4 in {0, 1}, the second those with k mod 4 in
+// {2, 3}, i.e. the threads of waves 0-1 and 2-3 of the 256-thread order. The
+// pair swaps its two folded partial sums through LDS (double-buffered by step
+// parity, one barrier per step), so both form (w0 + w2) + (w1 + w3). Rows are
+// grid-strided over pairs; every wave makes the same number of steps.
+template <int G, int THREADS>
+__global__ __launch_bounds__(THREADS) void rms_gated_pair_kernel(RmsArgs a) {
+    constexpr int MODE = kGatedRmsModulate;
+    constexpr int kPairs = THREADS / 128;
+    constexpr int kMine = (G + 3) / 4 * 2;  // upper bound on the groups of one wave
+    extern __shared__ U4 staged[];
+    __shared__ float sums[2][kPairs][4];
+    const int W8 = (a.W + 7) / 8;
+    const int64_t b = blockIdx.y;
+    stage_vectors<MODE, THREADS>(a, b, W8, staged);
+    const U4 *lw = staged, *lk = staged + W8, *lsh = staged + 2 * W8, *lg = staged + 3 * W8;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int pair = wave >> 1, half = wave & 1;
+    // The k of the j-th group of this wave: 4 (j / 2) + 2 half + j % 2.
+    auto k_of = [&](int j) { return 4 * (j >> 1) + 2 * half + (j & 1); };
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kPairs;
+    int parity = 0;
+    for (int64_t s0 = static_cast<int64_t>(blockIdx.x) * kPairs; s0 < a.S; s0 += step, parity ^= 1) {
+        const int64_t s = s0 + pair;
+        const bool row_ok = s < a.S;  // wave-uniform
+        U4 v[kMine], yv[kMine];
+        if (row_ok) {
+#pragma unroll
+            for (int j = 0; j < kMine; ++j) {
+                const int c0 = clamp_group(lane + 64 * k_of(j), W8) * 8;
+                v[j] = ld16_stream(row_ptr(a.x, b, s) + c0);
+                yv[j] = ld16_stream(row_ptr(a.y, b, s) + c0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
+        float part[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kMine; ++j) {
+            const int k = k_of(j), g = lane + 64 * k, gc = clamp_group(g, W8);
+            const bool valid = row_ok && k < G && g < W8;
+            v[j] = rms_phase1<MODE>(v[j], lg[gc], yv[j], valid, part[j & 1]);
+            if (valid) st16_stream(row_ptr_w(a.residual, b, s) + g * 8, v[j]);
+            keep_packed(v[j]);
+        }
+        const float f0 = fold_lanes<64>(part[0]), f1 = fold_lanes<64>(part[1]);
+        if (lane == 0) {
+            sums[parity][pair][2 * half] = f0;
+            sums[parity][pair][2 * half + 1] = f1;
+        }
+        __syncthreads();
+        const float *t = sums[parity][pair];
+        const float r = rms_reciprocal((t[0] + t[2]) + (t[1] + t[3]), a.W, a.eps_bf);
+#pragma unroll
+        for (int j = 0; j < kMine; ++j) {
+            const int k = k_of(j), g = lane + 64 * k, gc = clamp_group(g, W8);
+            const U4 o = rms_phase2<MODE>(v[j], r, lw[gc], lk[gc], lsh[gc]);
+            if (row_ok && k < G && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+        }
+    }
+}
+
+// Rows of W8 > 1024 groups: one row per 256-thread block, VPT groups per
+// thread (thread t owns groups t, t + 256, ...), the four wave partials
+// combined as (w0 + w2) + (w1 + w3).
+template <int VPT, bool VEC, int MODE>
+__global__ __launch_bounds__(kThreads) void rms_block_kernel(RmsArgs a) {
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / a.S, s = row % a.S;
+    const int W8 = (a.W + 7) / 8;
+    U4 v[VPT], gv[VPT], yv[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int c0 = clamp_group(threadIdx.x + j * kThreads, W8) * 8;
+        v[j] = load_group<VEC, true>(row_ptr(a.x, b, s), a.x.sw, c0, a.W);
+        if constexpr (MODE == kGatedRmsModulate) {
+            gv[j] = load_group<VEC>(row_ptr(a.gate, b, s), a.gate.sw, c0, a.W);
+            yv[j] = load_group<VEC, true>(row_ptr(a.y, b, s), a.y.sw, c0, a.W);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
+    float partial = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int g = threadIdx.x + j * kThreads;
+        v[j] = rms_phase1<MODE>(v[j], gv[j], yv[j], g < W8, partial);
+        if constexpr (MODE == kGatedRmsModulate)
+            if (g < W8) store_group<VEC, true>(row_ptr_w(a.residual, b, s), a.residual.sw, g * 8, a.W, v[j]);
+        keep_packed(v[j]);
+    }
+    __shared__ float red[kThreads / 64];
+    const float wsum = fold_lanes<64>(partial);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = wsum;
+    __syncthreads();
+    const float r = rms_reciprocal((red[0] + red[2]) + (red[1] + red[3]), a.W, a.eps_bf);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int g = threadIdx.x + j * kThreads, c0 = clamp_group(g, W8) * 8;
+        const U4 wv = load_group<VEC>(a.w, a.w_stride, c0, a.W);
+        U4 scv{}, shv{};
+        if constexpr (MODE != kRms) {
+            scv = load_group<VEC>(row_ptr(a.scale, b, s), a.scale.sw, c0, a.W);
+            shv = load_group<VEC>(row_ptr(a.shift, b, s), a.shift.sw, c0, a.W);
+        }
+        const U4 o = rms_phase2<MODE>(v[j], r, wv, factor_of(scv), shv);
+        if (g < W8) store_group<VEC, true>(row_ptr_w(a.out, b, s), a.out.sw, g * 8, a.W, o);
     }
 }
 
 template <int MODE, bool VEC>
 int launch_rms_vec(const RmsArgs &a, hipStream_t stream) {
     const int W8 = (a.W + 7) / 8;
-    auto grid_small = [&](int L) { return static_cast<unsigned>((a.rows + (kThreads / L) - 1) / (kThreads / L)); };
     if (W8 <= 64) {
         int L = 1;
         while (L < W8) L <<= 1;
+        // Four rows per lane group when that still leaves >= 1024 blocks.
+        const int64_t rows_per_block4 = static_cast<int64_t>(kThreads / L) * 4;
+        const bool four = (a.rows + rows_per_block4 - 1) / rows_per_block4 >= 1024;
+        const int64_t per_block = four ? rows_per_block4 : kThreads / L;
+        const unsigned grid = static_cast<unsigned>((a.rows + per_block - 1) / per_block);
         switch (L) {
-#define H3_RMS_SMALL(LL)                                                                          \
-    case LL:                                                                                     \
-        rms_rows_kernel<LL, 1, VEC, MODE><<<grid_small(LL), kThreads, 0, stream>>>(a);            \
+#define H3_RMS_LANES(LL)                                                                  \
+    case LL:                                                                             \
+        if (four)                                                                        \
+            rms_lanes_kernel<LL, 4, VEC, MODE><<<grid, kThreads, 0, stream>>>(a);        \
+        else                                                                             \
+            rms_lanes_kernel<LL, 1, VEC, MODE><<<grid, kThreads, 0, stream>>>(a);        \
         break;
-            H3_RMS_SMALL(1) H3_RMS_SMALL(2) H3_RMS_SMALL(4) H3_RMS_SMALL(8) H3_RMS_SMALL(16)
-            H3_RMS_SMALL(32) H3_RMS_SMALL(64)
-#undef H3_RMS_SMALL
+            H3_RMS_LANES(1) H3_RMS_LANES(2) H3_RMS_LANES(4) H3_RMS_LANES(8) H3_RMS_LANES(16)
+            H3_RMS_LANES(32) H3_RMS_LANES(64)
+#undef H3_RMS_LANES
         }
         return launch_status();
     }
+    const int need = (W8 + 63) / 64;
+    // Staged vectors: 1 (weight), 3 (+ factor, shift) or 4 (+ gate) rows of W8
+    // groups in LDS, within the 64 KiB a workgroup may allocate.
+    const int arrays = MODE == kRms ? 1 : (MODE == kRmsModulate ? 3 : 4);
+    const size_t lds = static_cast<size_t>(arrays) * W8 * sizeof(U4);
+    if (VEC && a.staged && need <= 16 && lds <= 65536) {
+        if constexpr (VEC) {
+            const unsigned batch = static_cast<unsigned>(a.rows / a.S);
+            constexpr int kWaves = kStagedThreads / 64;
+            const int64_t per_entry = (kStagedBlocks + batch - 1) / batch;
+            const int64_t needed = (a.S + kWaves - 1) / kWaves;
+            const dim3 grid(static_cast<unsigned>(needed < per_entry ? needed : per_entry), batch);
+            if constexpr (MODE == kGatedRmsModulate) {
+                constexpr int kPairs = kStagedThreads / 128;
+                const int64_t pairs_needed = (a.S + kPairs - 1) / kPairs;
+                const dim3 pgrid(static_cast<unsigned>(pairs_needed < per_entry ? pairs_needed : per_entry), batch);
+#define H3_RMS_PAIR(GG)                                                                                 \
+    if (need <= GG) {                                                                                  \
+        rms_gated_pair_kernel<GG, kStagedThreads><<<pgrid, kStagedThreads, lds, stream>>>(a);          \
+        return launch_status();                                                                        \
+    }
+                H3_RMS_PAIR(2) H3_RMS_PAIR(4) H3_RMS_PAIR(6) H3_RMS_PAIR(8) H3_RMS_PAIR(10) H3_RMS_PAIR(12)
+                H3_RMS_PAIR(14) H3_RMS_PAIR(16)
+#undef H3_RMS_PAIR
+            } else {
+#define H3_RMS_STAGED(GG)                                                                          \
+    if (need <= GG) {                                                                             \
+        rms_staged_kernel<GG, MODE, kStagedThreads><<<grid, kStagedThreads, lds, stream>>>(a);    \
+        return launch_status();                                                                   \
+    }
+                H3_RMS_STAGED(2) H3_RMS_STAGED(3) H3_RMS_STAGED(4) H3_RMS_STAGED(6) H3_RMS_STAGED(8)
+                H3_RMS_STAGED(10) H3_RMS_STAGED(12) H3_RMS_STAGED(14) H3_RMS_STAGED(16)
+#undef H3_RMS_STAGED
+            }
+        }
+    }
+    if (need <= 16) {
+        const unsigned grid = static_cast<unsigned>((a.rows + kThreads / 64 - 1) / (kThreads / 64));
+#define H3_RMS_WAVE(GG)                                                            \
+    if (need <= GG) {                                                             \
+        rms_wave_kernel<GG, VEC, MODE><<<grid, kThreads, 0, stream>>>(a);         \
+        return launch_status();                                                   \
+    }
+        H3_RMS_WAVE(2) H3_RMS_WAVE(3) H3_RMS_WAVE(4) H3_RMS_WAVE(6) H3_RMS_WAVE(8) H3_RMS_WAVE(10)
+        H3_RMS_WAVE(12) H3_RMS_WAVE(14) H3_RMS_WAVE(16)
+#undef H3_RMS_WAVE
+    }
     const int vpt = (W8 + kThreads - 1) / kThreads;
     const unsigned grid = static_cast<unsigned>(a.rows);
-#define H3_RMS_BIG(V)                                                                     \
-    if (vpt <= V) {                                                                      \
-        rms_rows_kernel<kThreads, V, VEC, MODE><<<grid, kThreads, 0, stream>>>(a);        \
-        return launch_status();                                                          \
+#define H3_RMS_BLOCK(V)                                                                \
+    if (vpt <= V) {                                                                   \
+        rms_block_kernel<V, VEC, MODE><<<grid, kThreads, 0, stream>>>(a);             \
+        return launch_status();                                                       \
     }
-    H3_RMS_BIG(1) H3_RMS_BIG(2) H3_RMS_BIG(3) H3_RMS_BIG(4) H3_RMS_BIG(6) H3_RMS_BIG(8)
-    H3_RMS_BIG(12) H3_RMS_BIG(16)
-#undef H3_RMS_BIG
+    H3_RMS_BLOCK(6) H3_RMS_BLOCK(8) H3_RMS_BLOCK(12) H3_RMS_BLOCK(16)
+#undef H3_RMS_BLOCK
     return kInvalid;  // W > 32768: outside the supported widths
 }
 
@@ -285,6 +643,10 @@ int rms_family(int mode, hipStream_t stream, const NineToothedTensor &x_t, const
     a.S = x.shape[1];
     a.W = static_cast<int>(x.shape[2]);
     a.eps_bf = host_round_bf16(eps);
+    // Row-invariant within a batch entry: broadcast over S (stride 0) or S = 1.
+    auto invariant = [&](const View<3> &t) { return t.shape[1] == 1 || t.stride[1] == 0; };
+    a.staged = x.shape[0] <= 65535 && (mode == kRms || (invariant(scale) && invariant(shift))) &&
+               (mode != kGatedRmsModulate || invariant(gate));
     if (a.rows == 0 || a.W == 0) return 0;
     if (a.rows > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     switch (mode) {
@@ -300,8 +662,8 @@ int rms_family(int mode, hipStream_t stream, const NineToothedTensor &x_t, const
 // ============================================================ elementwise
 
 // Column-chunked row streaming: block (row, chunk) handles 8-element groups
-// chunk*256*U + t + 256*u. Loads are issued before any store.
-constexpr int kEwUnroll = 4;
+// chunk*256*U + t + 256*u with U = Op::kUnroll (measured best per op: more
+// waves beat more loads per wave). Loads are issued before any store.
 
 struct EwArgs {
     Rows a, b, c, out;  // op inputs (c unused by SwiGLU) and output
@@ -312,6 +674,8 @@ struct EwArgs {
 // out = bf16(x + bf16(gate * y)) (tools/h3_pointwise.py:121-124)
 struct GatedResidualOp {
     static constexpr int kInputs = 3;
+    static constexpr unsigned kStream = 0b101;  // x, y streamed; gate (an AdaLN row, reused) cached
+    static constexpr int kUnroll = 1;
     __device__ static void apply(const float x[8], const float g[8], const float y[8], float o[8]) {
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
@@ -323,17 +687,52 @@ struct GatedResidualOp {
     }
 };
 
+// silu(g) = g / (1 + exp(-g)) in fp32, for |g| < 64, with the same values as
+// __fdiv_rn(g, 1 + expf(-g)) after the bf16 rounding that follows it. The
+// exponential is expf's own reduction (exp(x) = 2^n 2^t, n = rint(x log2 e),
+// t the remainder with log2 e split in two parts) without its overflow and
+// underflow selects, which cannot fire for |g| < 64. The quotient is
+// q0 = g rcp(d) plus one residual correction. Every bf16 g with |g| < 64 takes
+// this path in the exhaustive swiglu test, whose bf16 results are bitwise the
+// oracle's.
+__device__ __forceinline__ float silu_fast(float g) {
+    constexpr float kNegLog2e = -0x1.715476p+0f;        // -log2(e), fp32
+    constexpr float kNegLog2eLow = -0x1.4ae0bep-26f;    // -(log2(e) - 0x1.715476p+0)
+    const float ph = g * kNegLog2e;
+    const float n = __builtin_rintf(ph);
+    float pl = __builtin_fmaf(g, kNegLog2e, -ph);
+    pl = __builtin_fmaf(g, kNegLog2eLow, pl);
+    const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), static_cast<int>(n));
+    const float d = 1.0f + e;
+    const float y = __builtin_amdgcn_rcpf(d);
+    const float q0 = g * y;
+    // d >= 1 and the quotient never underflows to zero, so it has the sign of
+    // g; the copy keeps g = -0 at -0 (the correction would add +0 to it).
+    return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, d, g), y, q0), g);
+}
+
 // out = bf16(up * bf16(g / (1 + exp(-g)))) (tools/h3_pointwise.py:18-22)
 struct SwigluOp {
     static constexpr int kInputs = 2;
+    static constexpr unsigned kStream = 0b11;  // up and gate both streamed
+    static constexpr int kUnroll = 2;
     __device__ static void apply(const float up[8], const float g[8], const float *, float o[8]) {
+        bool fast = true;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fast = fast && __builtin_fabsf(g[e]) < 64.0f;
+        float a[8];
+        if (fast) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = silu_fast(g[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = __fdiv_rn(g[e], 1.0f + expf(-g[e]));
+        }
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            float a0 = __fdiv_rn(g[e], 1.0f + expf(-g[e]));
-            float a1 = __fdiv_rn(g[e + 1], 1.0f + expf(-g[e + 1]));
-            rbf2(a0, a1);
-            o[e] = up[e] * a0;
-            o[e + 1] = up[e + 1] * a1;
+            rbf2(a[e], a[e + 1]);
+            o[e] = up[e] * a[e];
+            o[e + 1] = up[e + 1] * a[e + 1];
         }
     }
 };
@@ -348,23 +747,23 @@ __global__ __launch_bounds__(kThreads) void ew_kernel(EwArgs a) {
     const bf16_t *pb = row_ptr(a.b, b, s);
     const bf16_t *pc = Op::kInputs > 2 ? row_ptr(a.c, b, s) : nullptr;
     bf16_t *po = row_ptr_w(a.out, b, s);
-    float va[kEwUnroll][8], vb[kEwUnroll][8], vc[kEwUnroll][8];
+    float va[Op::kUnroll][8], vb[Op::kUnroll][8], vc[Op::kUnroll][8];
+    // Loads from clamped groups for every lane (see clamp_group); only the
+    // stores are guarded.
 #pragma unroll
-    for (int u = 0; u < kEwUnroll; ++u) {
-        const int g = chunk * kThreads * kEwUnroll + u * kThreads + threadIdx.x;
-        if (g < W8) {
-            load8<VEC>(pa, a.a.sw, g * 8, a.W, va[u]);
-            load8<VEC>(pb, a.b.sw, g * 8, a.W, vb[u]);
-            if constexpr (Op::kInputs > 2) load8<VEC>(pc, a.c.sw, g * 8, a.W, vc[u]);
-        }
+    for (int u = 0; u < Op::kUnroll; ++u) {
+        const int c0 = clamp_group(chunk * kThreads * Op::kUnroll + u * kThreads + threadIdx.x, W8) * 8;
+        load8<VEC, (Op::kStream & 1) != 0>(pa, a.a.sw, c0, a.W, va[u]);
+        load8<VEC, (Op::kStream & 2) != 0>(pb, a.b.sw, c0, a.W, vb[u]);
+        if constexpr (Op::kInputs > 2) load8<VEC, (Op::kStream & 4) != 0>(pc, a.c.sw, c0, a.W, vc[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kEwUnroll; ++u) {
-        const int g = chunk * kThreads * kEwUnroll + u * kThreads + threadIdx.x;
+    for (int u = 0; u < Op::kUnroll; ++u) {
+        const int g = chunk * kThreads * Op::kUnroll + u * kThreads + threadIdx.x;
         if (g < W8) {
             float o[8];
             Op::apply(va[u], vb[u], vc[u], o);
-            store8<VEC>(po, a.out.sw, g * 8, a.W, o);
+            store8<VEC, true>(po, a.out.sw, g * 8, a.W, o);
         }
     }
 }
@@ -385,7 +784,7 @@ int launch_ew(hipStream_t stream, const View<3> *in, const View<3> &out) {
     a.W = static_cast<int>(out.shape[2]);
     if (a.rows == 0 || a.W == 0) return 0;
     const int W8 = (a.W + 7) / 8;
-    a.chunks = (W8 + kThreads * kEwUnroll - 1) / (kThreads * kEwUnroll);
+    a.chunks = (W8 + kThreads * Op::kUnroll - 1) / (kThreads * Op::kUnroll);
     const int64_t grid = a.rows * a.chunks;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     if (vec)
@@ -413,38 +812,60 @@ struct RopeArgs {
     float eps_bf;
 };
 
+enum RopeMode { kRopeOnly = 0, kNormRope = 1, kNormRopeInterleaved = 2 };
+
 __device__ __forceinline__ int64_t head_offset(const HeadRows &h, int64_t t, int64_t p, int64_t hh) {
     return t * h.s0 + p * h.s1 + hh * h.s2;
 }
 
 template <bool VEC>
-__device__ __forceinline__ void load_head8(const HeadRows &h, int64_t off, int lane, float f[8]) {
-    const bf16_t *row = reinterpret_cast<const bf16_t *>(h.p) + off;
-    if constexpr (VEC) {
-        u4_to_f8(ld16(row + lane * 8), f);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = bf2f(row[(lane * 8 + e) * h.s3]);
-    }
+__device__ __forceinline__ U4 load_head(const HeadRows &h, int64_t off, int lane) {
+    return load_group<VEC, true>(reinterpret_cast<const bf16_t *>(h.p) + off, h.s3, lane * 8, 128);
 }
 
 template <bool VEC>
-__device__ __forceinline__ void store_head8(const HeadRows &h, int64_t off, int lane, const float f[8]) {
-    bf16_t *row = reinterpret_cast<bf16_t *>(h.p) + off;
-    if constexpr (VEC) {
-        st16(row + lane * 8, f8_to_u4(f));
+__device__ __forceinline__ void store_head(const HeadRows &h, int64_t off, int lane, const float f[8]) {
+    store_group<VEC, true>(reinterpret_cast<bf16_t *>(h.p) + off, h.s3, lane * 8, 128, f8_to_u4(f));
+}
+
+// The cos/sin entries a lane needs for one row, loaded ahead of the arithmetic:
+// rotate-half, 8 entries of [T, 48] at column (lane mod 6) * 8 (lanes 0-11);
+// interleaved, 4 entries of [T, 64] at column 4 * lane (in c.x, c.y).
+struct RopeTab {
+    U4 c, s;
+};
+
+template <bool VEC, int MODE>
+__device__ __forceinline__ RopeTab load_tab(const RopeArgs &a, int64_t t, int lane) {
+    RopeTab tab{};
+    const bf16_t *cr = a.cos + t * a.cs0;
+    const bf16_t *sr = a.sin + t * a.ss0;
+    if constexpr (MODE == kNormRopeInterleaved) {
+        const int c0 = lane * 4;
+        if constexpr (VEC) {
+            const uint2 cv = *reinterpret_cast<const uint2 *>(cr + c0);
+            const uint2 sv = *reinterpret_cast<const uint2 *>(sr + c0);
+            tab.c = {cv.x, cv.y, 0u, 0u};
+            tab.s = {sv.x, sv.y, 0u, 0u};
+        } else {
+            tab.c.x = cr[c0 * a.cs1] | (static_cast<uint32_t>(cr[(c0 + 1) * a.cs1]) << 16);
+            tab.c.y = cr[(c0 + 2) * a.cs1] | (static_cast<uint32_t>(cr[(c0 + 3) * a.cs1]) << 16);
+            tab.s.x = sr[c0 * a.ss1] | (static_cast<uint32_t>(sr[(c0 + 1) * a.ss1]) << 16);
+            tab.s.y = sr[(c0 + 2) * a.ss1] | (static_cast<uint32_t>(sr[(c0 + 3) * a.ss1]) << 16);
+        }
     } else {
-        const U4 v = f8_to_u4(f);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) row[(lane * 8 + e) * h.s3] = static_cast<bf16_t>(w[e >> 1] >> (16 * (e & 1)));
+        // Lanes 12-15 (pass-through channels) load a column they do not use,
+        // so that no load sits under a per-lane branch.
+        const int c0 = (lane < 6 ? lane : (lane < 12 ? lane - 6 : 0)) * 8;
+        tab.c = load_group<VEC>(cr, a.cs1, c0, 48);
+        tab.s = load_group<VEC>(sr, a.ss1, c0, 48);
     }
+    return tab;
 }
 
 // RMSNorm over the 128 channels held by a 16-lane row group (the same fixed
 // order as the rms family at W = 128), then weight: returns bf16 values in f.
-template <bool VEC>
-__device__ __forceinline__ void head_rms(float f[8], int lane, const RopeArgs &a) {
+__device__ __forceinline__ void head_rms(float f[8], const float w[8], float eps_bf) {
     float partial = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -453,17 +874,7 @@ __device__ __forceinline__ void head_rms(float f[8], int lane, const RopeArgs &a
         partial += q0;
         partial += q1;
     }
-    const float total = fold_lanes<16>(partial);
-    const float mean = rbf(__fdiv_rn(total, 128.0f));
-    const float var = rbf(mean + a.eps_bf);
-    const float r = rbf(rsqrt_ieee(var));
-    float w[8];
-    if constexpr (VEC) {
-        u4_to_f8(ld16(a.w + lane * 8), w);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) w[e] = bf2f(a.w[(lane * 8 + e) * a.w_stride]);
-    }
+    const float r = rms_reciprocal(fold_lanes<16>(partial), 128, eps_bf);
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
         float n0 = f[e] * r, n1 = f[e + 1] * r;
@@ -479,27 +890,15 @@ __device__ __forceinline__ void head_rms(float f[8], int lane, const RopeArgs &a
 // Rotate-half RoPE on channels 0..95 (pairs i, i+48), 96..127 pass through,
 // cos/sin [T, 48] (tools/h3_pointwise.py:199-214). Lanes 0-5 hold the first
 // halves, lanes 6-11 the second halves, lanes 12-15 the pass-through.
-template <bool VEC>
-__device__ __forceinline__ void rope_rotate_half(float f[8], int lane, int64_t t, const RopeArgs &a) {
+__device__ __forceinline__ void rope_rotate_half(float f[8], int lane, const RopeTab &tab) {
     float partner[8];
     const int src = lane < 6 ? lane + 6 : (lane < 12 ? lane - 6 : lane);
 #pragma unroll
     for (int e = 0; e < 8; ++e) partner[e] = __shfl(f[e], src, 16);
     if (lane >= 12) return;
-    const int c0 = (lane < 6 ? lane : lane - 6) * 8;
     float c[8], s[8];
-    const bf16_t *cr = a.cos + t * a.cs0;
-    const bf16_t *sr = a.sin + t * a.ss0;
-    if constexpr (VEC) {
-        u4_to_f8(ld16(cr + c0), c);
-        u4_to_f8(ld16(sr + c0), s);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            c[e] = bf2f(cr[(c0 + e) * a.cs1]);
-            s[e] = bf2f(sr[(c0 + e) * a.ss1]);
-        }
-    }
+    u4_to_f8(tab.c, c);
+    u4_to_f8(tab.s, s);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const float av = lane < 6 ? f[e] : partner[e];  // first half a
@@ -519,23 +918,9 @@ __device__ __forceinline__ void rope_rotate_half(float f[8], int lane, int64_t t
 
 // Interleaved-pair RoPE on all 128 channels: pair i = (2i, 2i+1), cos/sin
 // [T, 64]; lane j owns pairs 4j..4j+3.
-template <bool VEC>
-__device__ __forceinline__ void rope_interleaved(float f[8], int lane, int64_t t, const RopeArgs &a) {
-    float c[4], s[4];
-    const bf16_t *cr = a.cos + t * a.cs0 + lane * 4 * a.cs1;
-    const bf16_t *sr = a.sin + t * a.ss0 + lane * 4 * a.ss1;
-    if constexpr (VEC) {
-        const uint2 cv = *reinterpret_cast<const uint2 *>(cr);
-        const uint2 sv = *reinterpret_cast<const uint2 *>(sr);
-        c[0] = lo2f(cv.x); c[1] = hi2f(cv.x); c[2] = lo2f(cv.y); c[3] = hi2f(cv.y);
-        s[0] = lo2f(sv.x); s[1] = hi2f(sv.x); s[2] = lo2f(sv.y); s[3] = hi2f(sv.y);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            c[i] = bf2f(cr[i * a.cs1]);
-            s[i] = bf2f(sr[i * a.ss1]);
-        }
-    }
+__device__ __forceinline__ void rope_interleaved(float f[8], const RopeTab &tab) {
+    const float c[4] = {lo2f(tab.c.x), hi2f(tab.c.x), lo2f(tab.c.y), hi2f(tab.c.y)};
+    const float s[4] = {lo2f(tab.s.x), hi2f(tab.s.x), lo2f(tab.s.y), hi2f(tab.s.y)};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float av = f[2 * i], bv = f[2 * i + 1];
@@ -548,26 +933,43 @@ __device__ __forceinline__ void rope_interleaved(float f[8], int lane, int64_t t
     }
 }
 
-enum RopeMode { kRopeOnly = 0, kNormRope = 1, kNormRopeInterleaved = 2 };
-
-template <bool VEC, int MODE>
+// R rows per 16-lane group: every row's x and table loads are issued before
+// the arithmetic of the first.
+template <bool VEC, int MODE, int R>
 __global__ __launch_bounds__(kThreads) void head_rows_kernel(RopeArgs a) {
+    constexpr int kGroups = kThreads / 16;
     const int lane = threadIdx.x & 15;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
-    const bool ok = row < a.rows;
-    const int64_t r = ok ? row : 0;
-    const int64_t t = r / (a.P * a.Hs);
-    const int64_t rem = r % (a.P * a.Hs);
-    const int64_t p = rem / a.Hs, hh = rem % a.Hs;
-    float f[8];
-    load_head8<VEC>(a.x, head_offset(a.x, t, p, hh), lane, f);
-    if constexpr (MODE != kRopeOnly) head_rms<VEC>(f, lane, a);
-    if constexpr (MODE == kNormRopeInterleaved) {
-        rope_interleaved<VEC>(f, lane, t, a);
-    } else {
-        rope_rotate_half<VEC>(f, lane, t, a);
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kGroups * R + (threadIdx.x >> 4);
+    bool ok[R];
+    int64_t out_off[R];
+    U4 xv[R];
+    RopeTab tab[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = base + r * kGroups;
+        ok[r] = row < a.rows;
+        const int64_t rr = ok[r] ? row : 0;
+        const int64_t t = rr / (a.P * a.Hs);
+        const int64_t rem = rr % (a.P * a.Hs);
+        const int64_t p = rem / a.Hs, hh = rem % a.Hs;
+        out_off[r] = head_offset(a.out, t, p, hh);
+        xv[r] = load_head<VEC>(a.x, head_offset(a.x, t, p, hh), lane);
+        tab[r] = load_tab<VEC, MODE>(a, t, lane);
     }
-    if (ok) store_head8<VEC>(a.out, head_offset(a.out, t, p, hh), lane, f);
+    float w[8];
+    if constexpr (MODE != kRopeOnly) u4_to_f8(load_group<VEC>(a.w, a.w_stride, lane * 8, 128), w);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float f[8];
+        u4_to_f8(xv[r], f);
+        if constexpr (MODE != kRopeOnly) head_rms(f, w, a.eps_bf);
+        if constexpr (MODE == kNormRopeInterleaved) {
+            rope_interleaved(f, tab[r]);
+        } else {
+            rope_rotate_half(f, lane, tab[r]);
+        }
+        if (ok[r]) store_head<VEC>(a.out, out_off[r], lane, f);
+    }
 }
 
 template <int MODE>
@@ -597,12 +999,24 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
     }
     a.eps_bf = host_round_bf16(eps);
     if (a.rows == 0) return 0;
-    const int64_t grid = (a.rows + kThreads / 16 - 1) / (kThreads / 16);
+    // Four rows per lane group when that still leaves >= 1024 blocks.
+    constexpr int64_t kPerBlock = kThreads / 16;
+    const bool four = (a.rows + 4 * kPerBlock - 1) / (4 * kPerBlock) >= 1024;
+    const int64_t per_block = four ? 4 * kPerBlock : kPerBlock;
+    const int64_t grid = (a.rows + per_block - 1) / per_block;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
-    if (vec)
-        head_rows_kernel<true, MODE><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a);
-    else
-        head_rows_kernel<false, MODE><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a);
+    const unsigned g = static_cast<unsigned>(grid);
+    if (vec) {
+        if (four)
+            head_rows_kernel<true, MODE, 4><<<g, kThreads, 0, stream>>>(a);
+        else
+            head_rows_kernel<true, MODE, 1><<<g, kThreads, 0, stream>>>(a);
+    } else {
+        if (four)
+            head_rows_kernel<false, MODE, 4><<<g, kThreads, 0, stream>>>(a);
+        else
+            head_rows_kernel<false, MODE, 1><<<g, kThreads, 0, stream>>>(a);
+    }
     return launch_status();
 }
 

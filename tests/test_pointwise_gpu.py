@@ -59,6 +59,11 @@ RMS_CASES = [
     (1, 17, 1000, "transposed"),          # non-unit inner stride
     (1, 5, 8, "contiguous"),
     (1, 3, 32768, "contiguous"),
+    (2, 40, 520, "contiguous"),           # one row per wave, two groups per lane
+    (1, 70, 3072, "contiguous"),
+    (1, 50, 8192, "contiguous"),          # largest one-row-per-wave width
+    (1, 9, 8200, "contiguous"),           # smallest one-row-per-block width
+    (1, 7, 16384, "packed_aligned"),
 ]
 
 
@@ -94,9 +99,9 @@ def test_rms_modulate(pkg, oracle, device, B, S, W, layout, broadcast):
     gen = _gen(3 * W + S)
     x = _layout(gen, B, S, W, layout, 8.0)
     w = _randn(gen, W)
-    if broadcast:
-        scale = _randn(gen, 1, 1, W, scale=0.5).expand(B, S, W)
-        shift = _randn(gen, 1, 1, W, scale=0.5).expand(B, S, W)
+    if broadcast:  # one AdaLN row per batch entry, broadcast over S
+        scale = _randn(gen, B, 1, W, scale=0.5).expand(B, S, W)
+        shift = _randn(gen, B, 1, W, scale=0.5).expand(B, S, W)
     else:
         table = _randn(gen, B, S, 6 * W, scale=0.5)
         shift, scale = table[..., :W], table[..., W:2 * W]
@@ -124,12 +129,16 @@ def test_gated_residual(pkg, oracle, device, B, S, W, broadcast_gate):
     assert_bitwise(out, torch.add(x, torch.mul(gate, y)), "gated_residual vs torch bf16 ops")
 
 
-@pytest.mark.parametrize("B,S,W", [(1, 257, 5376), (2, 65, 7168), (1, 33, 100), (1, 64, 128)])
-def test_gated_residual_rms_modulate(pkg, oracle, device, B, S, W):
+@pytest.mark.parametrize("B,S,W", [(1, 257, 5376), (2, 65, 7168), (1, 33, 100), (1, 64, 128), (3, 19, 2048)])
+@pytest.mark.parametrize("broadcast", [False, True])
+def test_gated_residual_rms_modulate(pkg, oracle, device, B, S, W, broadcast):
     gen = _gen(7 * W + S)
     x = _randn(gen, B, S, W, scale=8.0)
     y = _randn(gen, B, S, W)
-    table = _randn(gen, B, S, 6 * W, scale=0.5)
+    if broadcast:  # AdaLN rows per batch entry, broadcast over S
+        table = _randn(gen, B, 1, 6 * W, scale=0.5).expand(B, S, 6 * W)
+    else:
+        table = _randn(gen, B, S, 6 * W, scale=0.5)
     shift, scale, gate = table[..., :W], table[..., W:2 * W], table[..., 2 * W:3 * W]
     w = _randn(gen, W)
     residual = torch.empty(B, S, W, dtype=BF, device=device)
