@@ -56,6 +56,7 @@ constexpr int kRowV = kD + 32;
 constexpr int kTileElemsK = kBN * kRowK;
 constexpr int kTileElemsV = kBN * kRowV;
 constexpr int kLoadRows = kBN * 16 / kThreadsWG;  // 16-byte chunks per thread per tile
+static_assert(kBN * 16 % kThreadsWG == 0, "a tile is an exact number of chunks per thread");
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -78,27 +79,29 @@ __device__ __forceinline__ int xcd_remap(int x, int total) {
 }
 
 // Global -> registers for one 64-key tile of K or V: thread t loads rows
-// t/16 + (threads/16) r, 16-byte chunk t%16. Rows past `valid` are zero.
+// t/16 + (threads/16) r, 16-byte chunk t%16. Rows past `valid` re-read row
+// valid-1: every load is issued unconditionally (a load under a branch is
+// waited for before the branch closes), and the softmax masks those keys
+// (their scores become -inf and their probabilities exactly 0, which leaves
+// the finite V rows without effect). The registers are native vectors, so
+// the copies stay in registers.
 __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid,
-                                          uint4 reg[kLoadRows]) {
+                                          u32x4_t (&reg)[kLoadRows]) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r) {
-        const int row = t / 16 + (kThreadsWG / 16) * r;
-        if (row < valid) {
-            reg[r] = *reinterpret_cast<const uint4 *>(base + static_cast<int64_t>(key0 + row) * s_stride + (t % 16) * 8);
-        } else {
-            reg[r] = make_uint4(0, 0, 0, 0);
-        }
+        const int row0 = t / 16 + (kThreadsWG / 16) * r;
+        const int row = row0 < valid ? row0 : valid - 1;
+        reg[r] = *reinterpret_cast<const u32x4_t *>(base + static_cast<int64_t>(key0 + row) * s_stride + (t % 16) * 8);
     }
 }
 
 template <int PITCH>
-__device__ __forceinline__ void store_tile(bf16_t *lds, const uint4 reg[kLoadRows]) {
+__device__ __forceinline__ void store_tile(bf16_t *lds, const u32x4_t (&reg)[kLoadRows]) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r)
-        *reinterpret_cast<uint4 *>(lds + (t / 16 + (kThreadsWG / 16) * r) * PITCH + (t % 16) * 8) = reg[r];
+        *reinterpret_cast<u32x4_t *>(lds + (t / 16 + (kThreadsWG / 16) * r) * PITCH + (t % 16) * 8) = reg[r];
 }
 
 // One 64-key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK marks the
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         l_run[qs] = 0.0f;  // running denominator
     }
 
-    uint4 kreg[kLoadRows], vreg[kLoadRows];
+    u32x4_t kreg[kLoadRows], vreg[kLoadRows];
     load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
     load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
     store_tile<kRowK>(lds_k[0], kreg);
@@ -296,10 +299,13 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         const int buf = tile & 1;
         const int next0 = (tile + 1) * kBN;
         const bool has_next = next0 < a.Sk;
-        if (has_next) {
-            const int nvalid = a.Sk - next0 < kBN ? a.Sk - next0 : kBN;
-            load_tile(kbase, a.ks[2], next0, nvalid, kreg);
-            load_tile(vbase, a.vs[2], next0, nvalid, vreg);
+        {
+            // After the last tile the loads re-read the last row (unused), so
+            // they need no branch either.
+            const int n0 = has_next ? next0 : a.Sk - 1;
+            const int nvalid = a.Sk - n0 < kBN ? a.Sk - n0 : kBN;
+            load_tile(kbase, a.ks[2], n0, nvalid, kreg);
+            load_tile(vbase, a.vs[2], n0, nvalid, vreg);
         }
         attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, a.c, krow, half, v_row_off,
                                 v_col_off);
