@@ -24,6 +24,8 @@
 //
 // LDS tiles carry no padding; 16-byte chunks are XOR-swizzled per row so the
 // rows read by one 16-lane ds_read_b128 pass fall in distinct banks.
+#include <type_traits>
+
 #include "h3_common.hpp"
 
 namespace h3 {
@@ -98,6 +100,25 @@ __device__ __forceinline__ void load_k(const Fp8Args &a, int b, int h, int key0,
     }
 }
 
+// A full K tile: the loads of load_k without the row test, so the main loop
+// issues them unconditionally (a load under a branch is waited for before the
+// branch closes).
+template <bool QK_FP8>
+__device__ __forceinline__ void load_k_full(const Fp8Args &a, int b, int h, int key0, uint4 (&reg)[2]) {
+    const int t = threadIdx.x;
+    constexpr int kChunks = QK_FP8 ? 8 : 16;
+    constexpr int kPerThread = kBN * kChunks / kThreadsWG;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int idx = t + i * kThreadsWG;
+        const int r = idx / kChunks, c = idx % kChunks;
+        const uint8_t *row = QK_FP8
+            ? a.k8 + b * a.ks[0] + h * a.ks[1] + static_cast<int64_t>(key0 + r) * a.ks[2]
+            : reinterpret_cast<const uint8_t *>(a.k + b * a.ks[0] + h * a.ks[1] + static_cast<int64_t>(key0 + r) * a.ks[2]);
+        reg[i] = *reinterpret_cast<const uint4 *>(row + 16 * c);
+    }
+}
+
 template <bool QK_FP8>
 __device__ __forceinline__ void store_k(uint8_t *lds, const uint4 (&reg)[2]) {
     const int t = threadIdx.x;
@@ -125,6 +146,13 @@ __device__ __forceinline__ void load_v(const Fp8Args &a, int b, int h, int key0,
         for (int e = 0; e < 16; ++e) bytes[e] = (16 * c + e < valid) ? row[e] : 0;
         reg = *reinterpret_cast<const uint4 *>(bytes);
     }
+}
+
+// A full V^T tile: every 16-byte chunk is inside the 64 keys.
+__device__ __forceinline__ void load_v_full(const Fp8Args &a, int b, int h, int key0, uint4 &reg) {
+    const int t = threadIdx.x;
+    const int d = t / 4, c = t % 4;
+    reg = *reinterpret_cast<const uint4 *>(a.v8 + b * a.vs0 + h * a.vs1 + static_cast<int64_t>(d) * a.vs3 + key0 + 16 * c);
 }
 
 __device__ __forceinline__ void store_v(uint8_t *lds, const uint4 &reg) {
@@ -196,7 +224,126 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
     }
     __syncthreads();
 
-    for (int tile = 0; tile < ntiles; ++tile) {
+    // One tile of keys from LDS buffer `buf`: S^T = K Q^T, online softmax, O^T
+    // += V^T P^T. MASKED: keys >= valid are excluded (the last, partial tile).
+    auto attend = [&](auto masked_tag, int buf, int valid) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+            const uint8_t *kt = lds_k[buf];
+            const uint8_t *vt = lds_v[buf];
+
+            // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
+            f32x16_t s[2];
+            const f32x16_t zero = {};
+    #pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int r = key_of_row(ks, l32);
+                if constexpr (QK_FP8) {
+    #pragma unroll
+                    for (int kk = 0; kk < 2; ++kk) {
+                        const int c0 = 4 * kk + 2 * half;  // 16-byte chunk of dims 64kk + 32half
+                        const uint4 lo = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0));
+                        const uint4 hi = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0 + 1));
+                        const i32x8_t kop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                                          static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                          static_cast<int>(hi.z), static_cast<int>(hi.w)};
+                        s[ks] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q8reg[kk], kk == 0 ? zero : s[ks], 0,
+                                                                                0, 0, kScale1, 0, kScale1);
+                    }
+                } else {
+    #pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) {
+                        const int c0 = 2 * kk + half;  // 16-byte chunk of dims 16kk + 8half
+                        const bf16x8_t kop =
+                            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(kt + r * 256 + 16 * kswz16(r, c0)));
+                        s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qbreg[kk], kk == 0 ? zero : s[ks], 0, 0, 0);
+                    }
+                }
+            }
+
+            // ---- online softmax (this lane's query)
+            if constexpr (MASKED) {
+    #pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+    #pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (32 * half + 16 * ks + i >= valid) s[ks][i] = NEG ? INFINITY : -INFINITY;
+            }
+            float mx = s[0][0];
+    #pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+    #pragma unroll
+                for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][i]) : fmaxf(mx, s[ks][i]);
+            {
+                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
+                mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
+            }
+            const float m_tile = mx * c;
+            const bool grow = m_tile > m_run;
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+                const float m_new = grow ? m_tile : m_run;
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_run *= alpha;
+    #pragma unroll
+                for (int db = 0; db < 4; ++db)
+    #pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+            }
+            float rowsum = 0.0f;
+            int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
+    #pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+    #pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
+                    if (MASKED && 32 * half + 16 * ks + i >= valid) p = 0.0f;
+                    s[ks][i] = p;
+                    rowsum += p;
+                }
+    #pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
+                    v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
+                    pk[4 * ks + w] = v;
+                }
+            }
+            {
+                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
+                rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            }
+            l_run += rowsum;
+            const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
+
+            // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
+    #pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int d = 32 * db + l32;
+                const uint4 lo = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half));
+                const uint4 hi = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half + 1));
+                const i32x8_t vop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                                  static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                  static_cast<int>(hi.z), static_cast<int>(hi.w)};
+                acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, pop, acc[db], 0, 0, 0, kScale1, 0, kScale1);
+            }
+    };
+    using Full = std::integral_constant<bool, false>;
+    using Partial = std::integral_constant<bool, true>;
+    const int full = a.Sk / kBN;  // tiles 0 .. full-1 hold 64 keys
+    int tile = 0;
+    // Main loop: the next tile is full, so its loads need no masks or branches.
+    for (; tile + 1 < full; ++tile) {
+        const int buf = tile & 1;
+        uint4 kr[2], vr;
+        load_k_full<QK_FP8>(a, b, h, (tile + 1) * kBN, kr);
+        load_v_full(a, b, h, (tile + 1) * kBN, vr);
+        attend(Full{}, buf, kBN);
+        store_k<QK_FP8>(lds_k[buf ^ 1], kr);
+        store_v(lds_v[buf ^ 1], vr);
+        __syncthreads();
+    }
+    // The last full tile (if any) and the partial tile (if any).
+    for (; tile < ntiles; ++tile) {
         const int buf = tile & 1;
         const int key0 = tile * kBN;
         const int valid = a.Sk - key0 < kBN ? a.Sk - key0 : kBN;
@@ -207,111 +354,15 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
             load_k<QK_FP8>(a, b, h, key0 + kBN, nvalid, kr);
             load_v(a, b, h, key0 + kBN, nvalid, vr);
         }
-        const uint8_t *kt = lds_k[buf];
-        const uint8_t *vt = lds_v[buf];
-
-        // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
-        f32x16_t s[2];
-        const f32x16_t zero = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int r = key_of_row(ks, l32);
-            if constexpr (QK_FP8) {
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int c0 = 4 * kk + 2 * half;  // 16-byte chunk of dims 64kk + 32half
-                    const uint4 lo = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0));
-                    const uint4 hi = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0 + 1));
-                    const i32x8_t kop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
-                                      static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
-                                      static_cast<int>(hi.z), static_cast<int>(hi.w)};
-                    s[ks] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q8reg[kk], kk == 0 ? zero : s[ks], 0,
-                                                                            0, 0, kScale1, 0, kScale1);
-                }
-            } else {
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk) {
-                    const int c0 = 2 * kk + half;  // 16-byte chunk of dims 16kk + 8half
-                    const bf16x8_t kop =
-                        __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(kt + r * 256 + 16 * kswz16(r, c0)));
-                    s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qbreg[kk], kk == 0 ? zero : s[ks], 0, 0, 0);
-                }
-            }
-        }
-
-        // ---- online softmax (this lane's query)
-        const bool masked = valid < kBN;
-        if (masked) {
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (32 * half + 16 * ks + i >= valid) s[ks][i] = NEG ? INFINITY : -INFINITY;
-        }
-        float mx = s[0][0];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][i]) : fmaxf(mx, s[ks][i]);
-        {
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-            const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
-            mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
-        }
-        const float m_tile = mx * c;
-        const bool grow = m_tile > m_run;
-        if (__builtin_amdgcn_ballot_w64(grow)) {
-            const float m_new = grow ? m_tile : m_run;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-        }
-        float rowsum = 0.0f;
-        int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
-                if (masked && 32 * half + 16 * ks + i >= valid) p = 0.0f;
-                s[ks][i] = p;
-                rowsum += p;
-            }
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
-                v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
-                pk[4 * ks + w] = v;
-            }
-        }
-        {
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
-            rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-        }
-        l_run += rowsum;
-        const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
-
-        // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = 32 * db + l32;
-            const uint4 lo = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half));
-            const uint4 hi = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half + 1));
-            const i32x8_t vop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
-                              static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
-                              static_cast<int>(hi.z), static_cast<int>(hi.w)};
-            acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, pop, acc[db], 0, 0, 0, kScale1, 0, kScale1);
-        }
-
+        if (valid < kBN)
+            attend(Partial{}, buf, valid);
+        else
+            attend(Full{}, buf, kBN);
         if (has_next) {
             store_k<QK_FP8>(lds_k[buf ^ 1], kr);
             store_v(lds_v[buf ^ 1], vr);
+            __syncthreads();
         }
-        __syncthreads();
     }
 
     if (query >= a.Sq) return;
