@@ -80,7 +80,7 @@ struct Fp8Args {
 // K tile, global -> LDS (through registers): 64 rows of 128 (fp8) or 256 (bf16)
 // bytes; rows past `valid` are zero.
 template <bool QK_FP8>
-__device__ __forceinline__ void load_k(const Fp8Args &a, int b, int h, int key0, int valid, uint4 (&reg)[2]) {
+__device__ __forceinline__ void load_k(const Fp8Args &a, int b, int h, int key0, int valid, u32x4_t (&reg)[2]) {
     const int t = threadIdx.x;
     constexpr int kChunks = QK_FP8 ? 8 : 16;
     constexpr int kPerThread = kBN * kChunks / kThreadsWG;  // 1 or 2
@@ -93,9 +93,9 @@ __device__ __forceinline__ void load_k(const Fp8Args &a, int b, int h, int key0,
                 ? a.k8 + b * a.ks[0] + h * a.ks[1] + static_cast<int64_t>(key0 + r) * a.ks[2]
                 : reinterpret_cast<const uint8_t *>(a.k + b * a.ks[0] + h * a.ks[1] +
                                                     static_cast<int64_t>(key0 + r) * a.ks[2]);
-            reg[i] = *reinterpret_cast<const uint4 *>(row + 16 * c);
+            reg[i] = *reinterpret_cast<const u32x4_t *>(row + 16 * c);
         } else {
-            reg[i] = make_uint4(0, 0, 0, 0);
+            reg[i] = u32x4_t{0u, 0u, 0u, 0u};
         }
     }
 }
@@ -104,7 +104,7 @@ __device__ __forceinline__ void load_k(const Fp8Args &a, int b, int h, int key0,
 // issues them unconditionally (a load under a branch is waited for before the
 // branch closes).
 template <bool QK_FP8>
-__device__ __forceinline__ void load_k_full(const Fp8Args &a, int b, int h, int key0, uint4 (&reg)[2]) {
+__device__ __forceinline__ void load_k_full(const Fp8Args &a, int b, int h, int key0, u32x4_t (&reg)[2]) {
     const int t = threadIdx.x;
     constexpr int kChunks = QK_FP8 ? 8 : 16;
     constexpr int kPerThread = kBN * kChunks / kThreadsWG;
@@ -115,12 +115,12 @@ __device__ __forceinline__ void load_k_full(const Fp8Args &a, int b, int h, int 
         const uint8_t *row = QK_FP8
             ? a.k8 + b * a.ks[0] + h * a.ks[1] + static_cast<int64_t>(key0 + r) * a.ks[2]
             : reinterpret_cast<const uint8_t *>(a.k + b * a.ks[0] + h * a.ks[1] + static_cast<int64_t>(key0 + r) * a.ks[2]);
-        reg[i] = *reinterpret_cast<const uint4 *>(row + 16 * c);
+        reg[i] = *reinterpret_cast<const u32x4_t *>(row + 16 * c);
     }
 }
 
 template <bool QK_FP8>
-__device__ __forceinline__ void store_k(uint8_t *lds, const uint4 (&reg)[2]) {
+__device__ __forceinline__ void store_k(uint8_t *lds, const u32x4_t (&reg)[2]) {
     const int t = threadIdx.x;
     constexpr int kChunks = QK_FP8 ? 8 : 16;
     constexpr int kPerThread = kBN * kChunks / kThreadsWG;
@@ -129,36 +129,36 @@ __device__ __forceinline__ void store_k(uint8_t *lds, const uint4 (&reg)[2]) {
         const int idx = t + i * kThreadsWG;
         const int r = idx / kChunks, c = idx % kChunks;
         const int pos = QK_FP8 ? kswz8(r, c) : kswz16(r, c);
-        *reinterpret_cast<uint4 *>(lds + r * (16 * kChunks) + 16 * pos) = reg[i];
+        *reinterpret_cast<u32x4_t *>(lds + r * (16 * kChunks) + 16 * pos) = reg[i];
     }
 }
 
 // V^T tile: 128 rows (dims) of 64 key bytes; keys past `valid` are zero.
-__device__ __forceinline__ void load_v(const Fp8Args &a, int b, int h, int key0, int valid, uint4 &reg) {
+__device__ __forceinline__ void load_v(const Fp8Args &a, int b, int h, int key0, int valid, u32x4_t &reg) {
     const int t = threadIdx.x;
     const int d = t / 4, c = t % 4;
     const uint8_t *row = a.v8 + b * a.vs0 + h * a.vs1 + static_cast<int64_t>(d) * a.vs3 + key0 + 16 * c;
     if (16 * c + 16 <= valid) {
-        reg = *reinterpret_cast<const uint4 *>(row);
+        reg = *reinterpret_cast<const u32x4_t *>(row);
     } else {
         uint8_t bytes[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) bytes[e] = (16 * c + e < valid) ? row[e] : 0;
-        reg = *reinterpret_cast<const uint4 *>(bytes);
+        reg = *reinterpret_cast<const u32x4_t *>(bytes);
     }
 }
 
 // A full V^T tile: every 16-byte chunk is inside the 64 keys.
-__device__ __forceinline__ void load_v_full(const Fp8Args &a, int b, int h, int key0, uint4 &reg) {
+__device__ __forceinline__ void load_v_full(const Fp8Args &a, int b, int h, int key0, u32x4_t &reg) {
     const int t = threadIdx.x;
     const int d = t / 4, c = t % 4;
-    reg = *reinterpret_cast<const uint4 *>(a.v8 + b * a.vs0 + h * a.vs1 + static_cast<int64_t>(d) * a.vs3 + key0 + 16 * c);
+    reg = *reinterpret_cast<const u32x4_t *>(a.v8 + b * a.vs0 + h * a.vs1 + static_cast<int64_t>(d) * a.vs3 + key0 + 16 * c);
 }
 
-__device__ __forceinline__ void store_v(uint8_t *lds, const uint4 &reg) {
+__device__ __forceinline__ void store_v(uint8_t *lds, const u32x4_t &reg) {
     const int t = threadIdx.x;
     const int d = t / 4, c = t % 4;
-    *reinterpret_cast<uint4 *>(lds + d * 64 + 16 * vswz(d, c)) = reg;
+    *reinterpret_cast<u32x4_t *>(lds + d * 64 + 16 * vswz(d, c)) = reg;
 }
 
 // ------------------------------------------------------------------ kernel
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
 
     const int ntiles = (a.Sk + kBN - 1) / kBN;
     {
-        uint4 kr[2], vr;
+        u32x4_t kr[2], vr;
         const int valid = a.Sk < kBN ? a.Sk : kBN;
         load_k<QK_FP8>(a, b, h, 0, valid, kr);
         load_v(a, b, h, 0, valid, vr);
@@ -234,11 +234,11 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
             // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
             f32x16_t s[2];
             const f32x16_t zero = {};
-    #pragma unroll
+#pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const int r = key_of_row(ks, l32);
                 if constexpr (QK_FP8) {
-    #pragma unroll
+#pragma unroll
                     for (int kk = 0; kk < 2; ++kk) {
                         const int c0 = 4 * kk + 2 * half;  // 16-byte chunk of dims 64kk + 32half
                         const uint4 lo = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0));
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                                                                                 0, 0, kScale1, 0, kScale1);
                     }
                 } else {
-    #pragma unroll
+#pragma unroll
                     for (int kk = 0; kk < 8; ++kk) {
                         const int c0 = 2 * kk + half;  // 16-byte chunk of dims 16kk + 8half
                         const bf16x8_t kop =
@@ -260,18 +260,38 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                 }
             }
 
+            // Bounded K operand window: a few LDS reads ahead of the MFMAs,
+            // so the operands do not all occupy registers at once.
+            if constexpr (QK_FP8) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+                for (int i = 0; i < 14; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            }
+
             // ---- online softmax (this lane's query)
             if constexpr (MASKED) {
-    #pragma unroll
+#pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 16; ++i)
                         if (32 * half + 16 * ks + i >= valid) s[ks][i] = NEG ? INFINITY : -INFINITY;
             }
             float mx = s[0][0];
-    #pragma unroll
+#pragma unroll
             for (int ks = 0; ks < 2; ++ks)
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][i]) : fmaxf(mx, s[ks][i]);
             {
                 auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
@@ -285,23 +305,23 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                 const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
                 m_run = m_new;
                 l_run *= alpha;
-    #pragma unroll
+#pragma unroll
                 for (int db = 0; db < 4; ++db)
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
             }
             float rowsum = 0.0f;
             int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
-    #pragma unroll
+#pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
                     if (MASKED && 32 * half + 16 * ks + i >= valid) p = 0.0f;
                     s[ks][i] = p;
                     rowsum += p;
                 }
-    #pragma unroll
+#pragma unroll
                 for (int w = 0; w < 4; ++w) {
                     int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
                     v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
@@ -316,7 +336,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
             const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
 
             // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
-    #pragma unroll
+#pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const int d = 32 * db + l32;
                 const uint4 lo = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half));
@@ -326,6 +346,14 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                                   static_cast<int>(hi.z), static_cast<int>(hi.w)};
                 acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, pop, acc[db], 0, 0, 0, kScale1, 0, kScale1);
             }
+            // Bounded V^T operand window.
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     };
     using Full = std::integral_constant<bool, false>;
     using Partial = std::integral_constant<bool, true>;
@@ -334,7 +362,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
     // Main loop: the next tile is full, so its loads need no masks or branches.
     for (; tile + 1 < full; ++tile) {
         const int buf = tile & 1;
-        uint4 kr[2], vr;
+        u32x4_t kr[2], vr;
         load_k_full<QK_FP8>(a, b, h, (tile + 1) * kBN, kr);
         load_v_full(a, b, h, (tile + 1) * kBN, vr);
         attend(Full{}, buf, kBN);
@@ -348,7 +376,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
         const int key0 = tile * kBN;
         const int valid = a.Sk - key0 < kBN ? a.Sk - key0 : kBN;
         const bool has_next = tile + 1 < ntiles;
-        uint4 kr[2], vr;
+        u32x4_t kr[2], vr;
         if (has_next) {
             const int nvalid = a.Sk - key0 - kBN < kBN ? a.Sk - key0 - kBN : kBN;
             load_k<QK_FP8>(a, b, h, key0 + kBN, nvalid, kr);
