@@ -228,125 +228,41 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
     // += V^T P^T. MASKED: keys >= valid are excluded (the last, partial tile).
     auto attend = [&](auto masked_tag, int buf, int valid) {
         constexpr bool MASKED = decltype(masked_tag)::value;
-            const uint8_t *kt = lds_k[buf];
-            const uint8_t *vt = lds_v[buf];
+        const uint8_t *kt = lds_k[buf];
+        const uint8_t *vt = lds_v[buf];
 
-            // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
-            f32x16_t s[2];
-            const f32x16_t zero = {};
+        // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
+        f32x16_t s[2];
+        const f32x16_t zero = {};
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int r = key_of_row(ks, l32);
-                if constexpr (QK_FP8) {
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) {
-                        const int c0 = 4 * kk + 2 * half;  // 16-byte chunk of dims 64kk + 32half
-                        const uint4 lo = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0));
-                        const uint4 hi = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0 + 1));
-                        const i32x8_t kop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
-                                          static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
-                                          static_cast<int>(hi.z), static_cast<int>(hi.w)};
-                        s[ks] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q8reg[kk], kk == 0 ? zero : s[ks], 0,
-                                                                                0, 0, kScale1, 0, kScale1);
-                    }
-                } else {
-#pragma unroll
-                    for (int kk = 0; kk < 8; ++kk) {
-                        const int c0 = 2 * kk + half;  // 16-byte chunk of dims 16kk + 8half
-                        const bf16x8_t kop =
-                            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(kt + r * 256 + 16 * kswz16(r, c0)));
-                        s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qbreg[kk], kk == 0 ? zero : s[ks], 0, 0, 0);
-                    }
-                }
-            }
-
-            // Bounded K operand window: a few LDS reads ahead of the MFMAs,
-            // so the operands do not all occupy registers at once.
+        for (int ks = 0; ks < 2; ++ks) {
+            const int r = key_of_row(ks, l32);
             if constexpr (QK_FP8) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int c0 = 4 * kk + 2 * half;  // 16-byte chunk of dims 64kk + 32half
+                    const uint4 lo = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0));
+                    const uint4 hi = *reinterpret_cast<const uint4 *>(kt + r * 128 + 16 * kswz8(r, c0 + 1));
+                    const i32x8_t kop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                                      static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                      static_cast<int>(hi.z), static_cast<int>(hi.w)};
+                    s[ks] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q8reg[kk], kk == 0 ? zero : s[ks], 0,
+                                                                            0, 0, kScale1, 0, kScale1);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             } else {
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-                for (int i = 0; i < 14; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int kk = 0; kk < 8; ++kk) {
+                    const int c0 = 2 * kk + half;  // 16-byte chunk of dims 16kk + 8half
+                    const bf16x8_t kop =
+                        __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(kt + r * 256 + 16 * kswz16(r, c0)));
+                    s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qbreg[kk], kk == 0 ? zero : s[ks], 0, 0, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             }
+        }
 
-            // ---- online softmax (this lane's query)
-            if constexpr (MASKED) {
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        if (32 * half + 16 * ks + i >= valid) s[ks][i] = NEG ? INFINITY : -INFINITY;
-            }
-            float mx = s[0][0];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][i]) : fmaxf(mx, s[ks][i]);
-            {
-                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-                const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
-                mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
-            }
-            const float m_tile = mx * c;
-            const bool grow = m_tile > m_run;
-            if (__builtin_amdgcn_ballot_w64(grow)) {
-                const float m_new = grow ? m_tile : m_run;
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                m_run = m_new;
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
-            }
-            float rowsum = 0.0f;
-            int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
-                    if (MASKED && 32 * half + 16 * ks + i >= valid) p = 0.0f;
-                    s[ks][i] = p;
-                    rowsum += p;
-                }
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
-                    v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
-                    pk[4 * ks + w] = v;
-                }
-            }
-            {
-                auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
-                rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-            }
-            l_run += rowsum;
-            const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
-
-            // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const int d = 32 * db + l32;
-                const uint4 lo = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half));
-                const uint4 hi = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half + 1));
-                const i32x8_t vop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
-                                  static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
-                                  static_cast<int>(hi.z), static_cast<int>(hi.w)};
-                acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, pop, acc[db], 0, 0, 0, kScale1, 0, kScale1);
-            }
-            // Bounded V^T operand window.
+        // Bounded K operand window: a few LDS reads ahead of the MFMAs,
+        // so the operands do not all occupy registers at once.
+        if constexpr (QK_FP8) {
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -354,6 +270,90 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        } else {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 14; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+
+        // ---- online softmax (this lane's query)
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (32 * half + 16 * ks + i >= valid) s[ks][i] = NEG ? INFINITY : -INFINITY;
+        }
+        float mx = s[0][0];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = NEG ? fminf(mx, s[ks][i]) : fmaxf(mx, s[ks][i]);
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            const float o0 = __uint_as_float(sw[0]), o1 = __uint_as_float(sw[1]);
+            mx = NEG ? fminf(o0, o1) : fmaxf(o0, o1);
+        }
+        const float m_tile = mx * c;
+        const bool grow = m_tile > m_run;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float m_new = grow ? m_tile : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
+        }
+        float rowsum = 0.0f;
+        int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
+                if (MASKED && 32 * half + 16 * ks + i >= valid) p = 0.0f;
+                s[ks][i] = p;
+                rowsum += p;
+            }
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
+                v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
+                pk[4 * ks + w] = v;
+            }
+        }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
+            rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        l_run += rowsum;
+        const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
+
+        // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 32 * db + l32;
+            const uint4 lo = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half));
+            const uint4 hi = *reinterpret_cast<const uint4 *>(vt + d * 64 + 16 * vswz(d, 2 * half + 1));
+            const i32x8_t vop{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                              static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                              static_cast<int>(hi.z), static_cast<int>(hi.w)};
+            acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, pop, acc[db], 0, 0, 0, kScale1, 0, kScale1);
+        }
+        // Bounded V^T operand window.
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     };
     using Full = std::integral_constant<bool, false>;
     using Partial = std::integral_constant<bool, true>;
