@@ -149,6 +149,12 @@ __device__ __forceinline__ void rms_epilogue(float f[8], float r, const float w[
 // Launch shape of rms_staged_kernel: waves per block and about how many blocks.
 constexpr int kStagedThreads = 512;
 constexpr int kStagedBlocks = 512;
+// rms_stream_kernel (the gated mode): blocks in all (two per CU, as many as the
+// staged vectors leave room for), rows in flight per block. Measured at
+// S = 8192, C = 7168 against rms_staged_kernel: the gated mode streams faster
+// (x and y per row need twice the registers), the others do not.
+constexpr int kStreamBlocks = 512;
+constexpr int kStreamDepth = 2;
 
 // Loads are issued for every lane from a valid address, and only the arithmetic
 // and the stores are guarded: a load under a per-lane branch is waited for
@@ -345,7 +351,7 @@ __device__ __forceinline__ void stage_vectors(const RmsArgs &a, int64_t b, int W
 // only global accesses are its stores.
 template <int G, int MODE, int THREADS>
 __global__ __launch_bounds__(THREADS) void rms_staged_kernel(RmsArgs a) {
-    static_assert(MODE != kGatedRmsModulate, "the gated mode runs as rms_gated_pair_kernel");
+    static_assert(MODE != kGatedRmsModulate, "the gated mode runs as rms_stream_kernel");
     extern __shared__ U4 staged[];
     const int W8 = (a.W + 7) / 8;
     const int64_t b = blockIdx.y;
@@ -396,66 +402,75 @@ __global__ __launch_bounds__(THREADS) void rms_staged_kernel(RmsArgs a) {
     }
 }
 
-// The gated mode of rms_staged_kernel with each row split over a pair of waves,
-// halving the registers that hold x and y: of the groups l + 64k, the first
-// wave takes those with k mod 4 in {0, 1}, the second those with k mod 4 in
-// {2, 3}, i.e. the threads of waves 0-1 and 2-3 of the 256-thread order. The
-// pair swaps its two folded partial sums through LDS (double-buffered by step
-// parity, one barrier per step), so both form (w0 + w2) + (w1 + w3). Rows are
-// grid-strided over pairs; every wave makes the same number of steps.
-template <int G, int THREADS>
-__global__ __launch_bounds__(THREADS) void rms_gated_pair_kernel(RmsArgs a) {
-    constexpr int MODE = kGatedRmsModulate;
-    constexpr int kPairs = THREADS / 128;
-    constexpr int kMine = (G + 3) / 4 * 2;  // upper bound on the groups of one wave
+// Rows whose weight, modulation and gate vectors are the same for every s of
+// a batch entry b: one row at a time per 256-thread block, thread t owning
+// groups t, t + 256, ... (the fixed order itself). The block stages the
+// vectors in LDS once, then walks the rows of entry b grid-strided with a ring
+// of DEPTH rows in registers (the loads of the next DEPTH - 1 rows are in
+// flight while a row is reduced and written), so the blocks stream a sliding
+// window of rows. The four wave partials meet in LDS (double-buffered by row
+// parity, one barrier per row).
+template <int VPT, int MODE, int DEPTH>
+__global__ __launch_bounds__(kThreads) void rms_stream_kernel(RmsArgs a) {
     extern __shared__ U4 staged[];
-    __shared__ float sums[2][kPairs][4];
+    __shared__ float red[2][kThreads / 64];
     const int W8 = (a.W + 7) / 8;
     const int64_t b = blockIdx.y;
-    stage_vectors<MODE, THREADS>(a, b, W8, staged);
+    stage_vectors<MODE, kThreads>(a, b, W8, staged);
     const U4 *lw = staged, *lk = staged + W8, *lsh = staged + 2 * W8, *lg = staged + 3 * W8;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int pair = wave >> 1, half = wave & 1;
-    // The k of the j-th group of this wave: 4 (j / 2) + 2 half + j % 2.
-    auto k_of = [&](int j) { return 4 * (j >> 1) + 2 * half + (j & 1); };
-    const int64_t step = static_cast<int64_t>(gridDim.x) * kPairs;
-    int parity = 0;
-    for (int64_t s0 = static_cast<int64_t>(blockIdx.x) * kPairs; s0 < a.S; s0 += step, parity ^= 1) {
-        const int64_t s = s0 + pair;
-        const bool row_ok = s < a.S;  // wave-uniform
-        U4 v[kMine], yv[kMine];
-        if (row_ok) {
+    const int64_t step = gridDim.x;
+    U4 xr[DEPTH][VPT], yr[DEPTH][VPT];
+    // Rows past the end (block-uniform) re-read the last row; only stores are guarded.
+    auto load_row = [&](int64_t s, U4 (&xv)[VPT], U4 (&yv)[VPT]) {
+        const int64_t sc = s < a.S ? s : a.S - 1;
 #pragma unroll
-            for (int j = 0; j < kMine; ++j) {
-                const int c0 = clamp_group(lane + 64 * k_of(j), W8) * 8;
-                v[j] = ld16_stream(row_ptr(a.x, b, s) + c0);
-                yv[j] = ld16_stream(row_ptr(a.y, b, s) + c0);
-            }
+        for (int j = 0; j < VPT; ++j) {
+            const int c0 = clamp_group(threadIdx.x + j * kThreads, W8) * 8;
+            xv[j] = ld16_stream(row_ptr(a.x, b, sc) + c0);
+            if constexpr (MODE == kGatedRmsModulate) yv[j] = ld16_stream(row_ptr(a.y, b, sc) + c0);
         }
-        __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
-        float part[2] = {0.0f, 0.0f};
+    };
+    auto finish_row = [&](int64_t s, int parity, U4 (&xv)[VPT], U4 (&yv)[VPT]) {
+        const bool ok = s < a.S;
+        float partial = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kMine; ++j) {
-            const int k = k_of(j), g = lane + 64 * k, gc = clamp_group(g, W8);
-            const bool valid = row_ok && k < G && g < W8;
-            v[j] = rms_phase1<MODE>(v[j], lg[gc], yv[j], valid, part[j & 1]);
-            if (valid) st16_stream(row_ptr_w(a.residual, b, s) + g * 8, v[j]);
-            keep_packed(v[j]);
+        for (int j = 0; j < VPT; ++j) {
+            const int g = threadIdx.x + j * kThreads, gc = clamp_group(g, W8);
+            U4 gv{};
+            if constexpr (MODE == kGatedRmsModulate) gv = lg[gc];
+            xv[j] = rms_phase1<MODE>(xv[j], gv, yv[j], g < W8, partial);
+            if constexpr (MODE == kGatedRmsModulate)
+                if (ok && g < W8) st16_stream(row_ptr_w(a.residual, b, s) + g * 8, xv[j]);
+            keep_packed(xv[j]);
         }
-        const float f0 = fold_lanes<64>(part[0]), f1 = fold_lanes<64>(part[1]);
-        if (lane == 0) {
-            sums[parity][pair][2 * half] = f0;
-            sums[parity][pair][2 * half + 1] = f1;
-        }
+        const float wsum = fold_lanes<64>(partial);
+        if ((threadIdx.x & 63) == 0) red[parity][threadIdx.x >> 6] = wsum;
         __syncthreads();
-        const float *t = sums[parity][pair];
+        const float *t = red[parity];
         const float r = rms_reciprocal((t[0] + t[2]) + (t[1] + t[3]), a.W, a.eps_bf);
 #pragma unroll
-        for (int j = 0; j < kMine; ++j) {
-            const int k = k_of(j), g = lane + 64 * k, gc = clamp_group(g, W8);
-            const U4 o = rms_phase2<MODE>(v[j], r, lw[gc], lk[gc], lsh[gc]);
-            if (row_ok && k < G && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+        for (int j = 0; j < VPT; ++j) {
+            const int g = threadIdx.x + j * kThreads, gc = clamp_group(g, W8);
+            U4 kv{}, shv{};
+            if constexpr (MODE != kRms) {
+                kv = lk[gc];
+                shv = lsh[gc];
+            }
+            const U4 o = rms_phase2<MODE>(xv[j], r, lw[gc], kv, shv);
+            if (ok && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+        }
+    };
+    const int64_t first = blockIdx.x;
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d) load_row(first + d * step, xr[d], yr[d]);
+    int parity = 0;
+    for (int64_t base = first; base < a.S; base += DEPTH * step) {  // same trip count in every wave
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int64_t s = base + d * step;
+            load_row(s + (DEPTH - 1) * step, xr[(d + DEPTH - 1) % DEPTH], yr[(d + DEPTH - 1) % DEPTH]);
+            finish_row(s, parity, xr[d], yr[d]);
+            parity ^= 1;
         }
     }
 }
@@ -537,26 +552,25 @@ int launch_rms_vec(const RmsArgs &a, hipStream_t stream) {
     // groups in LDS, within the 64 KiB a workgroup may allocate.
     const int arrays = MODE == kRms ? 1 : (MODE == kRmsModulate ? 3 : 4);
     const size_t lds = static_cast<size_t>(arrays) * W8 * sizeof(U4);
-    if (VEC && a.staged && need <= 16 && lds <= 65536) {
+    if (VEC && a.staged && lds <= 65536) {
         if constexpr (VEC) {
             const unsigned batch = static_cast<unsigned>(a.rows / a.S);
-            constexpr int kWaves = kStagedThreads / 64;
-            const int64_t per_entry = (kStagedBlocks + batch - 1) / batch;
-            const int64_t needed = (a.S + kWaves - 1) / kWaves;
-            const dim3 grid(static_cast<unsigned>(needed < per_entry ? needed : per_entry), batch);
             if constexpr (MODE == kGatedRmsModulate) {
-                constexpr int kPairs = kStagedThreads / 128;
-                const int64_t pairs_needed = (a.S + kPairs - 1) / kPairs;
-                const dim3 pgrid(static_cast<unsigned>(pairs_needed < per_entry ? pairs_needed : per_entry), batch);
-#define H3_RMS_PAIR(GG)                                                                                 \
-    if (need <= GG) {                                                                                  \
-        rms_gated_pair_kernel<GG, kStagedThreads><<<pgrid, kStagedThreads, lds, stream>>>(a);          \
-        return launch_status();                                                                        \
+                const int64_t per_entry = (kStreamBlocks + batch - 1) / batch;
+                const dim3 grid(static_cast<unsigned>(a.S < per_entry ? a.S : per_entry), batch);
+                const int vpt = (W8 + kThreads - 1) / kThreads;
+#define H3_RMS_STREAM(V)                                                                    \
+    if (vpt <= V) {                                                                        \
+        rms_stream_kernel<V, MODE, kStreamDepth><<<grid, kThreads, lds, stream>>>(a);     \
+        return launch_status();                                                            \
     }
-                H3_RMS_PAIR(2) H3_RMS_PAIR(4) H3_RMS_PAIR(6) H3_RMS_PAIR(8) H3_RMS_PAIR(10) H3_RMS_PAIR(12)
-                H3_RMS_PAIR(14) H3_RMS_PAIR(16)
-#undef H3_RMS_PAIR
-            } else {
+                H3_RMS_STREAM(1) H3_RMS_STREAM(2) H3_RMS_STREAM(3) H3_RMS_STREAM(4)
+#undef H3_RMS_STREAM
+            } else if (need <= 16) {
+                constexpr int kWaves = kStagedThreads / 64;
+                const int64_t per_entry = (kStagedBlocks + batch - 1) / batch;
+                const int64_t needed = (a.S + kWaves - 1) / kWaves;
+                const dim3 grid(static_cast<unsigned>(needed < per_entry ? needed : per_entry), batch);
 #define H3_RMS_STAGED(GG)                                                                          \
     if (need <= GG) {                                                                             \
         rms_staged_kernel<GG, MODE, kStagedThreads><<<grid, kStagedThreads, lds, stream>>>(a);    \
