@@ -151,6 +151,25 @@ def bench_pointwise(pkg, device) -> dict:
     ms = time_graph([lambda x=x, y=y, o=o, r=r: k_grm(x, gate, y, wC, 1e-6, scale, shift, r, o)
                      for x, y, o, r in zip(xs, ys, outs, res)])
     record("gated_residual_rms_modulate", ms, 4 * S * C * 2 + 4 * C * 2, [1, S, C])
+    # The same three ops with per-token AdaLN rows: two runs of tokens (1/8 and
+    # 7/8 of S) taking rows 0 and 1 of the [2, 6C] modulation matrix.
+    R = 2
+    cols = pkg.modulation_columns(rnd(R, 6 * C, scale=0.1), C)
+    index = torch.cat([torch.zeros(S // 8, dtype=torch.int64), torch.ones(S - S // 8, dtype=torch.int64)])
+    index = index.to(device).view(1, S)
+    tables = R * C * 2
+    k_mod_i = pkg.make_rms_modulate_indexed(check_indices=False)
+    ms = time_graph([lambda x=x, o=o: k_mod_i(x, wC, 1e-6, cols["scale_msa"], cols["shift_msa"], index, o)
+                     for x, o in zip(xs, outs)])
+    record("rms_modulate_indexed", ms, 2 * S * C * 2 + C * 2 + 2 * tables + S * 8, [1, S, C])
+    k_gr_i = pkg.make_gated_residual_indexed(check_indices=False)
+    ms = time_graph([lambda x=x, y=y, o=o: k_gr_i(x, cols["gate_mlp"], y, index, o) for x, y, o in zip(xs, ys, outs)])
+    record("gated_residual_indexed", ms, 3 * S * C * 2 + tables + S * 8, [1, S, C])
+    k_grm_i = pkg.make_gated_residual_rms_modulate_indexed(check_indices=False)
+    ms = time_graph([lambda x=x, y=y, o=o, r=r: k_grm_i(x, cols["gate_msa"], y, wC, 1e-6, cols["scale_mlp"],
+                                                        cols["shift_mlp"], index, r, o)
+                     for x, y, o, r in zip(xs, ys, outs, res)])
+    record("gated_residual_rms_modulate_indexed", ms, 4 * S * C * 2 + C * 2 + 3 * tables + S * 8, [1, S, C])
     del xs, ys, outs, res
     ups = [rnd(1, S, F) for _ in range(2)]
     gates = [rnd(1, S, F) for _ in range(2)]

@@ -153,6 +153,52 @@ NineToothedResult launch_h3_gated_residual_rms_modulate_exact(
     NineToothedTensor weight, NineToothedTensor eps, NineToothedTensor scale,
     NineToothedTensor shift, NineToothedTensor residual, NineToothedTensor out);
 
+/* ------------------------------------------- per-token AdaLN rows (indexed) */
+
+/* The three AdaLN ops of a DiT block over all tokens in ONE launch each, every
+ * token taking its own row of the modulation tables. The reference runs them
+ * once per run-length segment of its AdaLN indices, on stride-0 broadcast
+ * views of the segment's modulation row, after copying the indices to the
+ * host to build the segments (patches/InfiniLM.patch:1353-1397 per-segment
+ * launches, :1765-1793 segment construction); these entry points read the
+ * per-token indices on the device instead, with no host round trip, and give
+ * the same bits as the per-segment launches.
+ *
+ * Common arguments:
+ *   - x, y, out, residual: bf16 [B, S, W] as for the non-indexed entry points;
+ *   - scale, shift, gate: bf16 tables [R, W] (any row stride, e.g. column
+ *     blocks of the [R, 6 * W] modulation matrix: shift_msa 0, scale_msa 1,
+ *     gate_msa 2, shift_mlp 3, scale_mlp 4, gate_mlp 5, as at
+ *     patches/InfiniLM.patch:1375); all tables of one call have the same R >= 1;
+ *   - index: int64 [B, S] (any strides), token (b, s) uses row index[b, s] of
+ *     every table. Indices must lie in [0, R); the kernels clamp any other
+ *     value into that range so that no index reads outside the tables (the
+ *     reference's host-side narrow rejects them: callers that need the error
+ *     check the range before the launch).
+ * No single-launch counterpart in the reference; callers are the DiT block's
+ * AdaLN sites named above. */
+
+/* launch_h3_rms_modulate_exact with scale/shift rows index[b, s] of the tables. */
+NineToothedResult launch_h3_rms_modulate_indexed(NineToothedStream stream, NineToothedTensor x,
+                                                 NineToothedTensor weight, NineToothedTensor eps,
+                                                 NineToothedTensor scale, NineToothedTensor shift,
+                                                 NineToothedTensor index, NineToothedTensor out);
+
+/* launch_h3_gated_residual_rms_modulate_exact with gate/scale/shift rows
+ * index[b, s] of the tables. */
+NineToothedResult launch_h3_gated_residual_rms_modulate_indexed(
+    NineToothedStream stream, NineToothedTensor x, NineToothedTensor gate, NineToothedTensor y,
+    NineToothedTensor weight, NineToothedTensor eps, NineToothedTensor scale,
+    NineToothedTensor shift, NineToothedTensor index, NineToothedTensor residual,
+    NineToothedTensor out);
+
+/* launch_h3_gated_residual_exact with the gate row index[b, s] of the table. */
+NineToothedResult launch_h3_gated_residual_indexed(NineToothedStream stream, NineToothedTensor x,
+                                                   NineToothedTensor gate, NineToothedTensor y,
+                                                   NineToothedTensor index, NineToothedTensor out);
+
+/* ----------------------------------------------------------------- q/k + RoPE */
+
 /* Per-(token, head) RMSNorm over 128 channels (weight [128]) then the
  * rotate-half RoPE of launch_h3_rope_exact, on x [T, P, Hs, 128] (any strides)
  * written to out [T, P, Hs, 128] (any strides, e.g. a permuted all-to-all send

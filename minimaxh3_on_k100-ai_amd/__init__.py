@@ -16,14 +16,18 @@ from .h3_attention import (  # noqa: F401
 )
 from .h3_pointwise import (  # noqa: F401
     make_gated_residual,
+    make_gated_residual_indexed,
     make_gated_residual_rms_modulate,
+    make_gated_residual_rms_modulate_indexed,
     make_qk_norm_rope,
     make_qk_norm_rope_interleaved,
     make_rms,
     make_rms_modulate,
+    make_rms_modulate_indexed,
     make_rope,
     make_rope_cache,
     make_swiglu,
+    modulation_columns,
 )
 
 library = _lib.library

@@ -30,6 +30,9 @@ ENTRY_POINTS = {
     "launch_h3_rope_exact": 8,
     "launch_h3_gated_residual_exact": 4,
     "launch_h3_gated_residual_rms_modulate_exact": 9,
+    "launch_h3_rms_modulate_indexed": 7,
+    "launch_h3_gated_residual_rms_modulate_indexed": 10,
+    "launch_h3_gated_residual_indexed": 5,
     "launch_h3_qk_norm_rope": 12,
     "launch_h3_qk_norm_rope_interleaved": 6,
     "launch_h3_rope_cache": 4,

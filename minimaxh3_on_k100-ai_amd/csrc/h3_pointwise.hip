@@ -103,6 +103,37 @@ __device__ __forceinline__ float fold_lanes(float v) {
 
 enum RmsMode { kRms = 0, kRmsModulate = 1, kGatedRmsModulate = 2 };
 
+// Per-token modulation rows: token (b, s) takes row p[b * sb + s * ss] of
+// [count, W] tables (scale, shift, gate). p == nullptr: the modulation views
+// are [B, S, W] like x and token (b, s) takes their row (b, s).
+struct ModIndex {
+    const int64_t *p;
+    int64_t sb, ss, count;
+};
+
+// A value every lane of the wave holds, moved to scalar registers so that
+// branches on it are uniform.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// The coordinates of token (b, s)'s modulation row in the modulation views:
+// (b, s) itself, or (index[b, s], 0) in the tables (a table is a Rows view with
+// its row stride in sb), the index clamped into [0, count) so that no value
+// of it reads outside the tables.
+__device__ __forceinline__ void mod_coords(const ModIndex &ix, int64_t b, int64_t s, int64_t &mb, int64_t &ms) {
+    if (ix.p == nullptr) {
+        mb = b;
+        ms = s;
+    } else {
+        const int64_t m = ix.p[b * ix.sb + s * ix.ss];
+        mb = m < 0 ? 0 : (m < ix.count ? m : ix.count - 1);
+        ms = 0;
+    }
+}
+
 struct RmsArgs {
     Rows x, gate, y, scale, shift, residual, out;
     const bf16_t *w;
@@ -111,6 +142,7 @@ struct RmsArgs {
     int W;
     float eps_bf;  // eps already rounded fp64 -> fp32 -> bf16
     bool staged;   // weight, scale, shift and gate are the same for every s of a batch entry
+    ModIndex index;  // gate, scale and shift rows per token (indexed entry points)
 };
 
 // bf16(1 + scale) of a group: the modulation factor, packed.
@@ -241,13 +273,15 @@ __global__ __launch_bounds__(kThreads) void rms_lanes_kernel(RmsArgs a) {
         b[r] = rr / a.S;
         s[r] = rr % a.S;
         xv[r] = load_group<VEC, true>(row_ptr(a.x, b[r], s[r]), a.x.sw, c0, a.W);
-        if constexpr (MODE == kGatedRmsModulate) {
-            gv[r] = load_group<VEC>(row_ptr(a.gate, b[r], s[r]), a.gate.sw, c0, a.W);
+        if constexpr (MODE == kGatedRmsModulate)
             yv[r] = load_group<VEC, true>(row_ptr(a.y, b[r], s[r]), a.y.sw, c0, a.W);
-        }
         if constexpr (MODE != kRms) {
-            scv[r] = load_group<VEC>(row_ptr(a.scale, b[r], s[r]), a.scale.sw, c0, a.W);
-            shv[r] = load_group<VEC>(row_ptr(a.shift, b[r], s[r]), a.shift.sw, c0, a.W);
+            int64_t mb, ms;
+            mod_coords(a.index, b[r], s[r], mb, ms);
+            if constexpr (MODE == kGatedRmsModulate)
+                gv[r] = load_group<VEC>(row_ptr(a.gate, mb, ms), a.gate.sw, c0, a.W);
+            scv[r] = load_group<VEC>(row_ptr(a.scale, mb, ms), a.scale.sw, c0, a.W);
+            shv[r] = load_group<VEC>(row_ptr(a.shift, mb, ms), a.shift.sw, c0, a.W);
         }
     }
     const U4 wv = load_group<VEC>(a.w, a.w_stride, c0, a.W);
@@ -277,6 +311,8 @@ __global__ __launch_bounds__(kThreads) void rms_wave_kernel(RmsArgs a) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
     if (row >= a.rows) return;  // whole waves only; no block-level synchronization below
     const int64_t b = row / a.S, s = row % a.S;
+    int64_t mb, ms;
+    mod_coords(a.index, b, s, mb, ms);
     const int W8 = (a.W + 7) / 8;
     U4 v[G], gv[G], yv[G];
 #pragma unroll
@@ -284,7 +320,7 @@ __global__ __launch_bounds__(kThreads) void rms_wave_kernel(RmsArgs a) {
         const int c0 = clamp_group(lane + 64 * k, W8) * 8;
         v[k] = load_group<VEC, true>(row_ptr(a.x, b, s), a.x.sw, c0, a.W);
         if constexpr (MODE == kGatedRmsModulate) {
-            gv[k] = load_group<VEC>(row_ptr(a.gate, b, s), a.gate.sw, c0, a.W);
+            gv[k] = load_group<VEC>(row_ptr(a.gate, mb, ms), a.gate.sw, c0, a.W);
             yv[k] = load_group<VEC, true>(row_ptr(a.y, b, s), a.y.sw, c0, a.W);
         }
     }
@@ -296,8 +332,8 @@ __global__ __launch_bounds__(kThreads) void rms_wave_kernel(RmsArgs a) {
             const int c0 = clamp_group(lane + 64 * (c * kChunk + j), W8) * 8;
             wv[c & 1][j] = load_group<VEC>(a.w, a.w_stride, c0, a.W);
             if constexpr (MODE != kRms) {
-                scv[c & 1][j] = load_group<VEC>(row_ptr(a.scale, b, s), a.scale.sw, c0, a.W);
-                shv[c & 1][j] = load_group<VEC>(row_ptr(a.shift, b, s), a.shift.sw, c0, a.W);
+                scv[c & 1][j] = load_group<VEC>(row_ptr(a.scale, mb, ms), a.scale.sw, c0, a.W);
+                shv[c & 1][j] = load_group<VEC>(row_ptr(a.shift, mb, ms), a.shift.sw, c0, a.W);
             }
         }
     };
@@ -410,28 +446,51 @@ __global__ __launch_bounds__(THREADS) void rms_staged_kernel(RmsArgs a) {
 // flight while a row is reduced and written), so the blocks stream a sliding
 // window of rows. The four wave partials meet in LDS (double-buffered by row
 // parity, one barrier per row).
-template <int VPT, int MODE, int DEPTH>
+//
+// INDEXED: every token names its modulation row (ModIndex). The blocks walk
+// all B * S rows grid-strided; a row's index is loaded with its data (one
+// value for the whole block), and the block stages that row of the tables
+// whenever it differs from the one in LDS -- once per run of equal indices a
+// block meets, since a block's rows are in token order.
+template <int VPT, int MODE, int DEPTH, bool INDEXED>
 __global__ __launch_bounds__(kThreads) void rms_stream_kernel(RmsArgs a) {
     extern __shared__ U4 staged[];
     __shared__ float red[2][kThreads / 64];
     const int W8 = (a.W + 7) / 8;
-    const int64_t b = blockIdx.y;
-    stage_vectors<MODE, kThreads>(a, b, W8, staged);
+    const int64_t count = INDEXED ? a.rows : a.S;  // rows this block's grid walks
+    const int64_t b0 = INDEXED ? 0 : blockIdx.y;
+    if constexpr (!INDEXED) stage_vectors<MODE, kThreads>(a, b0, W8, staged);
     const U4 *lw = staged, *lk = staged + W8, *lsh = staged + 2 * W8, *lg = staged + 3 * W8;
     const int64_t step = gridDim.x;
     U4 xr[DEPTH][VPT], yr[DEPTH][VPT];
+    int64_t mr[DEPTH];     // INDEXED: the modulation row of each row in the ring
+    int64_t in_lds = -1;   // INDEXED: the modulation row staged in LDS
     // Rows past the end (block-uniform) re-read the last row; only stores are guarded.
-    auto load_row = [&](int64_t s, U4 (&xv)[VPT], U4 (&yv)[VPT]) {
-        const int64_t sc = s < a.S ? s : a.S - 1;
+    auto load_row = [&](int64_t i, U4 (&xv)[VPT], U4 (&yv)[VPT], int64_t &m) {
+        const int64_t ic = i < count ? i : count - 1;
+        const int64_t b = INDEXED ? ic / a.S : b0, s = INDEXED ? ic % a.S : ic;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int c0 = clamp_group(threadIdx.x + j * kThreads, W8) * 8;
-            xv[j] = ld16_stream(row_ptr(a.x, b, sc) + c0);
-            if constexpr (MODE == kGatedRmsModulate) yv[j] = ld16_stream(row_ptr(a.y, b, sc) + c0);
+            xv[j] = ld16_stream(row_ptr(a.x, b, s) + c0);
+            if constexpr (MODE == kGatedRmsModulate) yv[j] = ld16_stream(row_ptr(a.y, b, s) + c0);
+        }
+        if constexpr (INDEXED) {
+            int64_t ms;
+            mod_coords(a.index, b, s, m, ms);
         }
     };
-    auto finish_row = [&](int64_t s, int parity, U4 (&xv)[VPT], U4 (&yv)[VPT]) {
-        const bool ok = s < a.S;
+    auto finish_row = [&](int64_t i, int parity, U4 (&xv)[VPT], U4 (&yv)[VPT], int64_t m) {
+        const bool ok = i < count;
+        const int64_t b = INDEXED ? i / a.S : b0, s = INDEXED ? i % a.S : i;
+        if constexpr (INDEXED) {
+            m = uniform64(m);  // every thread loaded the same index
+            if (m != in_lds) {
+                __syncthreads();  // the previous row's reads of the staged vectors are done
+                stage_vectors<MODE, kThreads>(a, m, W8, staged);
+                in_lds = m;
+            }
+        }
         float partial = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
@@ -462,14 +521,15 @@ __global__ __launch_bounds__(kThreads) void rms_stream_kernel(RmsArgs a) {
     };
     const int64_t first = blockIdx.x;
 #pragma unroll
-    for (int d = 0; d < DEPTH - 1; ++d) load_row(first + d * step, xr[d], yr[d]);
+    for (int d = 0; d < DEPTH - 1; ++d) load_row(first + d * step, xr[d], yr[d], mr[d]);
     int parity = 0;
-    for (int64_t base = first; base < a.S; base += DEPTH * step) {  // same trip count in every wave
+    for (int64_t base = first; base < count; base += DEPTH * step) {  // same trip count in every wave
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            const int64_t s = base + d * step;
-            load_row(s + (DEPTH - 1) * step, xr[(d + DEPTH - 1) % DEPTH], yr[(d + DEPTH - 1) % DEPTH]);
-            finish_row(s, parity, xr[d], yr[d]);
+            const int64_t i = base + d * step;
+            const int nd = (d + DEPTH - 1) % DEPTH;
+            load_row(i + (DEPTH - 1) * step, xr[nd], yr[nd], mr[nd]);
+            finish_row(i, parity, xr[d], yr[d], mr[d]);
             parity ^= 1;
         }
     }
@@ -482,6 +542,8 @@ template <int VPT, bool VEC, int MODE>
 __global__ __launch_bounds__(kThreads) void rms_block_kernel(RmsArgs a) {
     const int64_t row = blockIdx.x;
     const int64_t b = row / a.S, s = row % a.S;
+    int64_t mb, ms;
+    mod_coords(a.index, b, s, mb, ms);
     const int W8 = (a.W + 7) / 8;
     U4 v[VPT], gv[VPT], yv[VPT];
 #pragma unroll
@@ -489,7 +551,7 @@ __global__ __launch_bounds__(kThreads) void rms_block_kernel(RmsArgs a) {
         const int c0 = clamp_group(threadIdx.x + j * kThreads, W8) * 8;
         v[j] = load_group<VEC, true>(row_ptr(a.x, b, s), a.x.sw, c0, a.W);
         if constexpr (MODE == kGatedRmsModulate) {
-            gv[j] = load_group<VEC>(row_ptr(a.gate, b, s), a.gate.sw, c0, a.W);
+            gv[j] = load_group<VEC>(row_ptr(a.gate, mb, ms), a.gate.sw, c0, a.W);
             yv[j] = load_group<VEC, true>(row_ptr(a.y, b, s), a.y.sw, c0, a.W);
         }
     }
@@ -514,8 +576,8 @@ __global__ __launch_bounds__(kThreads) void rms_block_kernel(RmsArgs a) {
         const U4 wv = load_group<VEC>(a.w, a.w_stride, c0, a.W);
         U4 scv{}, shv{};
         if constexpr (MODE != kRms) {
-            scv = load_group<VEC>(row_ptr(a.scale, b, s), a.scale.sw, c0, a.W);
-            shv = load_group<VEC>(row_ptr(a.shift, b, s), a.shift.sw, c0, a.W);
+            scv = load_group<VEC>(row_ptr(a.scale, mb, ms), a.scale.sw, c0, a.W);
+            shv = load_group<VEC>(row_ptr(a.shift, mb, ms), a.shift.sw, c0, a.W);
         }
         const U4 o = rms_phase2<MODE>(v[j], r, wv, factor_of(scv), shv);
         if (g < W8) store_group<VEC, true>(row_ptr_w(a.out, b, s), a.out.sw, g * 8, a.W, o);
@@ -552,6 +614,21 @@ int launch_rms_vec(const RmsArgs &a, hipStream_t stream) {
     // groups in LDS, within the 64 KiB a workgroup may allocate.
     const int arrays = MODE == kRms ? 1 : (MODE == kRmsModulate ? 3 : 4);
     const size_t lds = static_cast<size_t>(arrays) * W8 * sizeof(U4);
+    if constexpr (VEC && MODE != kRms) {
+        // Per-token modulation rows: rms_stream_kernel over all rows, restaging
+        // the tables' row at each change of index.
+        const int vpt = (W8 + kThreads - 1) / kThreads;
+        if (a.index.p != nullptr && lds <= 65536 && vpt <= 4) {
+            const unsigned grid = static_cast<unsigned>(a.rows < kStreamBlocks ? a.rows : kStreamBlocks);
+#define H3_RMS_STREAM_INDEXED(V)                                                            \
+    if (vpt <= V) {                                                                        \
+        rms_stream_kernel<V, MODE, kStreamDepth, true><<<grid, kThreads, lds, stream>>>(a); \
+        return launch_status();                                                            \
+    }
+            H3_RMS_STREAM_INDEXED(1) H3_RMS_STREAM_INDEXED(2) H3_RMS_STREAM_INDEXED(3) H3_RMS_STREAM_INDEXED(4)
+#undef H3_RMS_STREAM_INDEXED
+        }
+    }
     if (VEC && a.staged && lds <= 65536) {
         if constexpr (VEC) {
             const unsigned batch = static_cast<unsigned>(a.rows / a.S);
@@ -561,7 +638,7 @@ int launch_rms_vec(const RmsArgs &a, hipStream_t stream) {
                 const int vpt = (W8 + kThreads - 1) / kThreads;
 #define H3_RMS_STREAM(V)                                                                    \
     if (vpt <= V) {                                                                        \
-        rms_stream_kernel<V, MODE, kStreamDepth><<<grid, kThreads, lds, stream>>>(a);     \
+        rms_stream_kernel<V, MODE, kStreamDepth, false><<<grid, kThreads, lds, stream>>>(a); \
         return launch_status();                                                            \
     }
                 H3_RMS_STREAM(1) H3_RMS_STREAM(2) H3_RMS_STREAM(3) H3_RMS_STREAM(4)
@@ -619,11 +696,39 @@ float host_round_bf16(double eps) {
     return f;
 }
 
+// A modulation operand (scale, shift, gate) as the kernels address it: a
+// [B, S, W] view shaped like x, or, with a per-token index, a [R, W] table
+// whose row r is addressed as (r, 0) (Rows with the row stride in sb). `vec`
+// drops to false when the operand cannot be read with 16-byte vectors;
+// `invariant` when its rows differ within a batch entry (views only);
+// `table_rows` takes R from the first table and checks the others against it.
+bool load_modulation(const NineToothedTensor &t, const View<3> &x, bool indexed, Rows &r, bool &vec,
+                     bool &invariant, int64_t &table_rows) {
+    if (!indexed) {
+        View<3> v;
+        if (!load_view(t, 2, v) || !same_shape(x, v)) return false;
+        r = rows_of(v);
+        vec = vec && rows_vec16(v, 2);
+        invariant = invariant && (v.shape[1] == 1 || v.stride[1] == 0);
+        return true;
+    }
+    View<2> v;
+    if (!load_view(t, 2, v) || v.shape[1] != x.shape[2]) return false;
+    if (table_rows < 0) table_rows = v.shape[0];
+    if (v.shape[0] != table_rows) return false;
+    r = {v.data, v.stride[0], 0, v.stride[1]};
+    vec = vec && rows_vec16(v, 2);
+    return true;
+}
+
+// The RMS family's launcher. `index_t` (indexed entry points only): int64
+// [B, S], token (b, s)'s row of the [R, W] gate / scale / shift tables.
 int rms_family(int mode, hipStream_t stream, const NineToothedTensor &x_t, const NineToothedTensor *gate_t,
                const NineToothedTensor *y_t, const NineToothedTensor &w_t, const NineToothedTensor &eps_t,
                const NineToothedTensor *scale_t, const NineToothedTensor *shift_t,
-               const NineToothedTensor *residual_t, const NineToothedTensor &out_t, int required_width) {
-    View<3> x, out, gate, y, scale, shift, residual;
+               const NineToothedTensor *residual_t, const NineToothedTensor &out_t, int required_width,
+               const NineToothedTensor *index_t = nullptr) {
+    View<3> x, out, y, residual;
     View<1> w;
     double eps;
     if (!load_view(x_t, 2, x) || !load_view(out_t, 2, out) || !load_view(w_t, 2, w) || !load_scalar(eps_t, eps))
@@ -632,25 +737,34 @@ int rms_family(int mode, hipStream_t stream, const NineToothedTensor &x_t, const
     if (required_width > 0 && x.shape[2] != required_width) return kInvalid;
     if (x.shape[2] > 32768) return kInvalid;
     bool vec = rows_vec16(x, 2) && rows_vec16(out, 2) && rows_vec16(w, 2);
+    RmsArgs a{};
+    const bool indexed = index_t != nullptr;
+    bool invariant = true;  // every modulation operand is the same for all s of a batch entry
+    int64_t table_rows = -1;
     if (mode == kGatedRmsModulate) {
-        if (!load_view(*gate_t, 2, gate) || !load_view(*y_t, 2, y) || !load_view(*residual_t, 2, residual))
-            return kInvalid;
-        if (!same_shape(x, gate) || !same_shape(x, y) || !same_shape(x, residual)) return kInvalid;
-        vec = vec && rows_vec16(gate, 2) && rows_vec16(y, 2) && rows_vec16(residual, 2);
+        if (!load_view(*y_t, 2, y) || !load_view(*residual_t, 2, residual)) return kInvalid;
+        if (!same_shape(x, y) || !same_shape(x, residual)) return kInvalid;
+        vec = vec && rows_vec16(y, 2) && rows_vec16(residual, 2);
+        if (!load_modulation(*gate_t, x, indexed, a.gate, vec, invariant, table_rows)) return kInvalid;
     }
     if (mode != kRms) {
-        if (!load_view(*scale_t, 2, scale) || !load_view(*shift_t, 2, shift)) return kInvalid;
-        if (!same_shape(x, scale) || !same_shape(x, shift)) return kInvalid;
-        vec = vec && rows_vec16(scale, 2) && rows_vec16(shift, 2);
+        if (!load_modulation(*scale_t, x, indexed, a.scale, vec, invariant, table_rows) ||
+            !load_modulation(*shift_t, x, indexed, a.shift, vec, invariant, table_rows))
+            return kInvalid;
     }
-    RmsArgs a{};
+    if (indexed) {
+        View<2> ix;
+        if (mode == kRms || !load_view(*index_t, 8, ix)) return kInvalid;
+        if (ix.shape[0] != x.shape[0] || ix.shape[1] != x.shape[1]) return kInvalid;
+        if (table_rows == 0 && x.numel() != 0) return kInvalid;  // no row for the tokens to take
+        a.index = {reinterpret_cast<const int64_t *>(ix.data), ix.stride[0], ix.stride[1], table_rows};
+    }
     a.x = rows_of(x);
     a.out = rows_of(out);
-    a.gate = mode == kGatedRmsModulate ? rows_of(gate) : a.x;
+    if (mode != kGatedRmsModulate) a.gate = a.x;
     a.y = mode == kGatedRmsModulate ? rows_of(y) : a.x;
     a.residual = mode == kGatedRmsModulate ? rows_of(residual) : a.out;
-    a.scale = mode != kRms ? rows_of(scale) : a.x;
-    a.shift = mode != kRms ? rows_of(shift) : a.x;
+    if (mode == kRms) a.scale = a.shift = a.x;
     a.w = reinterpret_cast<const bf16_t *>(w.data);
     a.w_stride = w.stride[0];
     a.rows = x.shape[0] * x.shape[1];
@@ -658,9 +772,7 @@ int rms_family(int mode, hipStream_t stream, const NineToothedTensor &x_t, const
     a.W = static_cast<int>(x.shape[2]);
     a.eps_bf = host_round_bf16(eps);
     // Row-invariant within a batch entry: broadcast over S (stride 0) or S = 1.
-    auto invariant = [&](const View<3> &t) { return t.shape[1] == 1 || t.stride[1] == 0; };
-    a.staged = x.shape[0] <= 65535 && (mode == kRms || (invariant(scale) && invariant(shift))) &&
-               (mode != kGatedRmsModulate || invariant(gate));
+    a.staged = !indexed && x.shape[0] <= 65535 && invariant;
     if (a.rows == 0 || a.W == 0) return 0;
     if (a.rows > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     switch (mode) {
@@ -683,6 +795,7 @@ struct EwArgs {
     Rows a, b, c, out;  // op inputs (c unused by SwiGLU) and output
     int64_t rows, S;
     int W, chunks;
+    ModIndex index;  // IDX kernels: token (b, s) reads row index[b, s] of the table `b`
 };
 
 // out = bf16(x + bf16(gate * y)) (tools/h3_pointwise.py:121-124)
@@ -690,6 +803,7 @@ struct GatedResidualOp {
     static constexpr int kInputs = 3;
     static constexpr unsigned kStream = 0b101;  // x, y streamed; gate (an AdaLN row, reused) cached
     static constexpr int kUnroll = 1;
+    static constexpr bool kIndexable = true;  // the gate may be a table row per token
     __device__ static void apply(const float x[8], const float g[8], const float y[8], float o[8]) {
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
@@ -730,6 +844,7 @@ struct SwigluOp {
     static constexpr int kInputs = 2;
     static constexpr unsigned kStream = 0b11;  // up and gate both streamed
     static constexpr int kUnroll = 2;
+    static constexpr bool kIndexable = false;
     __device__ static void apply(const float up[8], const float g[8], const float *, float o[8]) {
         bool fast = true;
 #pragma unroll
@@ -751,14 +866,16 @@ struct SwigluOp {
     }
 };
 
-template <class Op, bool VEC>
+template <class Op, bool VEC, bool IDX>
 __global__ __launch_bounds__(kThreads) void ew_kernel(EwArgs a) {
     const int64_t row = blockIdx.x / a.chunks;
     const int chunk = blockIdx.x % a.chunks;
     const int64_t b = row / a.S, s = row % a.S;
     const int W8 = (a.W + 7) / 8;
+    int64_t mb = b, ms = s;
+    if constexpr (IDX) mod_coords(a.index, b, s, mb, ms);
     const bf16_t *pa = row_ptr(a.a, b, s);
-    const bf16_t *pb = row_ptr(a.b, b, s);
+    const bf16_t *pb = row_ptr(a.b, mb, ms);
     const bf16_t *pc = Op::kInputs > 2 ? row_ptr(a.c, b, s) : nullptr;
     bf16_t *po = row_ptr_w(a.out, b, s);
     float va[Op::kUnroll][8], vb[Op::kUnroll][8], vc[Op::kUnroll][8];
@@ -782,16 +899,36 @@ __global__ __launch_bounds__(kThreads) void ew_kernel(EwArgs a) {
     }
 }
 
+// Launches Op over [B, S, W] views. With `index` (int64 [B, S]), input 1 is a
+// [R, W] table and token (b, s) reads its row index[b, s].
 template <class Op>
-int launch_ew(hipStream_t stream, const View<3> *in, const View<3> &out) {
-    for (int i = 0; i < Op::kInputs; ++i)
-        if (!same_shape(in[i], out)) return kInvalid;
+int launch_ew(hipStream_t stream, const NineToothedTensor *in_t, const NineToothedTensor &out_t,
+              const NineToothedTensor *index_t = nullptr) {
+    View<3> in[Op::kInputs], out;
+    if (!load_view(out_t, 2, out)) return kInvalid;
     bool vec = rows_vec16(out, 2);
-    for (int i = 0; i < Op::kInputs; ++i) vec = vec && rows_vec16(in[i], 2);
     EwArgs a{};
-    a.a = rows_of(in[0]);
-    a.b = rows_of(in[1]);
-    a.c = Op::kInputs > 2 ? rows_of(in[2]) : a.a;
+    Rows rows[Op::kInputs];
+    for (int i = 0; i < Op::kInputs; ++i) {
+        if (i == 1 && index_t != nullptr) {
+            View<2> table;
+            View<2> ix;
+            if (!load_view(in_t[i], 2, table) || table.shape[1] != out.shape[2]) return kInvalid;
+            if (!load_view(*index_t, 8, ix) || ix.shape[0] != out.shape[0] || ix.shape[1] != out.shape[1])
+                return kInvalid;
+            if (table.shape[0] == 0 && out.numel() != 0) return kInvalid;  // no row for the tokens to take
+            rows[i] = {table.data, table.stride[0], 0, table.stride[1]};
+            vec = vec && rows_vec16(table, 2);
+            a.index = {reinterpret_cast<const int64_t *>(ix.data), ix.stride[0], ix.stride[1], table.shape[0]};
+            continue;
+        }
+        if (!load_view(in_t[i], 2, in[i]) || !same_shape(in[i], out)) return kInvalid;
+        rows[i] = rows_of(in[i]);
+        vec = vec && rows_vec16(in[i], 2);
+    }
+    a.a = rows[0];
+    a.b = rows[1];
+    a.c = Op::kInputs > 2 ? rows[Op::kInputs - 1] : a.a;
     a.out = rows_of(out);
     a.rows = out.shape[0] * out.shape[1];
     a.S = out.shape[1];
@@ -801,10 +938,21 @@ int launch_ew(hipStream_t stream, const View<3> *in, const View<3> &out) {
     a.chunks = (W8 + kThreads * Op::kUnroll - 1) / (kThreads * Op::kUnroll);
     const int64_t grid = a.rows * a.chunks;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
-    if (vec)
-        ew_kernel<Op, true><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a);
-    else
-        ew_kernel<Op, false><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a);
+    const unsigned g = static_cast<unsigned>(grid);
+    if (index_t != nullptr) {
+        if constexpr (Op::kIndexable) {
+            if (vec)
+                ew_kernel<Op, true, true><<<g, kThreads, 0, stream>>>(a);
+            else
+                ew_kernel<Op, false, true><<<g, kThreads, 0, stream>>>(a);
+        } else {
+            return kInvalid;
+        }
+    } else if (vec) {
+        ew_kernel<Op, true, false><<<g, kThreads, 0, stream>>>(a);
+    } else {
+        ew_kernel<Op, false, false><<<g, kThreads, 0, stream>>>(a);
+    }
     return launch_status();
 }
 
@@ -1063,18 +1211,22 @@ extern "C" {
 
 NineToothedResult launch_h3_swiglu_exact(NineToothedStream stream, NineToothedTensor up, NineToothedTensor gate,
                                          NineToothedTensor out) {
-    View<3> in[2], o;
-    if (!load_view(up, 2, in[0]) || !load_view(gate, 2, in[1]) || !load_view(out, 2, o)) return kInvalid;
-    return launch_ew<SwigluOp>(as_stream(stream), in, o);
+    const NineToothedTensor in[2] = {up, gate};
+    return launch_ew<SwigluOp>(as_stream(stream), in, out);
 }
 
 NineToothedResult launch_h3_gated_residual_exact(NineToothedStream stream, NineToothedTensor x,
                                                  NineToothedTensor gate, NineToothedTensor y,
                                                  NineToothedTensor out) {
-    View<3> in[3], o;
-    if (!load_view(x, 2, in[0]) || !load_view(gate, 2, in[1]) || !load_view(y, 2, in[2]) || !load_view(out, 2, o))
-        return kInvalid;
-    return launch_ew<GatedResidualOp>(as_stream(stream), in, o);
+    const NineToothedTensor in[3] = {x, gate, y};
+    return launch_ew<GatedResidualOp>(as_stream(stream), in, out);
+}
+
+NineToothedResult launch_h3_gated_residual_indexed(NineToothedStream stream, NineToothedTensor x,
+                                                   NineToothedTensor gate, NineToothedTensor y,
+                                                   NineToothedTensor index, NineToothedTensor out) {
+    const NineToothedTensor in[3] = {x, gate, y};
+    return launch_ew<GatedResidualOp>(as_stream(stream), in, out, &index);
 }
 
 NineToothedResult launch_h3_rms_exact(NineToothedStream stream, NineToothedTensor x, NineToothedTensor weight,
@@ -1107,6 +1259,22 @@ NineToothedResult launch_h3_gated_residual_rms_modulate_exact(
     NineToothedTensor residual, NineToothedTensor out) {
     return rms_family(kGatedRmsModulate, as_stream(stream), x, &gate, &y, weight, eps, &scale, &shift, &residual,
                       out, 0);
+}
+
+NineToothedResult launch_h3_rms_modulate_indexed(NineToothedStream stream, NineToothedTensor x,
+                                                 NineToothedTensor weight, NineToothedTensor eps,
+                                                 NineToothedTensor scale, NineToothedTensor shift,
+                                                 NineToothedTensor index, NineToothedTensor out) {
+    return rms_family(kRmsModulate, as_stream(stream), x, nullptr, nullptr, weight, eps, &scale, &shift, nullptr,
+                      out, 0, &index);
+}
+
+NineToothedResult launch_h3_gated_residual_rms_modulate_indexed(
+    NineToothedStream stream, NineToothedTensor x, NineToothedTensor gate, NineToothedTensor y,
+    NineToothedTensor weight, NineToothedTensor eps, NineToothedTensor scale, NineToothedTensor shift,
+    NineToothedTensor index, NineToothedTensor residual, NineToothedTensor out) {
+    return rms_family(kGatedRmsModulate, as_stream(stream), x, &gate, &y, weight, eps, &scale, &shift, &residual,
+                      out, 0, &index);
 }
 
 NineToothedResult launch_h3_rope_exact(NineToothedStream stream, NineToothedTensor x0, NineToothedTensor x1,

@@ -17,7 +17,8 @@ from . import _lib
 __all__ = [
     "make_swiglu", "make_rms", "make_rms_modulate", "make_gated_residual",
     "make_gated_residual_rms_modulate", "make_rope", "make_qk_norm_rope",
-    "make_qk_norm_rope_interleaved", "make_rope_cache",
+    "make_qk_norm_rope_interleaved", "make_rope_cache", "modulation_columns", "make_rms_modulate_indexed",
+    "make_gated_residual_rms_modulate_indexed", "make_gated_residual_indexed",
 ]
 
 
@@ -113,6 +114,103 @@ def make_gated_residual_rms_modulate(caller="torch", output_dir=None, archs=None
         _lib.launch("launch_h3_gated_residual_rms_modulate_exact", device, _lib.tensor(x), _lib.tensor(gate),
                     _lib.tensor(y), _lib.tensor(weight), _lib.scalar(eps), _lib.tensor(scale),
                     _lib.tensor(shift), _lib.tensor(residual), _lib.tensor(out))
+
+    return kernel
+
+
+# ------------------------------------------------- per-token AdaLN rows (indexed)
+#
+# A DiT block's AdaLN sites over all tokens in one launch each, token (b, s)
+# taking row index[b, s] of the modulation tables. The reference launches each
+# op once per run-length segment of the indices, on broadcast views of the
+# segment's row (patches/InfiniLM.patch:1353-1397, segments built on the host
+# at :1765-1793); the results are the same bits.
+
+MODULATION_COLUMNS = ("shift_msa", "scale_msa", "gate_msa", "shift_mlp", "scale_mlp", "gate_mlp")
+
+
+def modulation_columns(modulation: torch.Tensor, hidden: int) -> dict:
+    """The six [R, hidden] column blocks of the AdaLN modulation matrix
+    [R, 6 * hidden], by name, in the reference's column order
+    (patches/InfiniLM.patch:1359-1364,1375): views, no copies."""
+    if modulation.dim() != 2 or modulation.shape[1] != 6 * hidden:
+        raise ValueError(f"modulation must be [R, 6 * {hidden}], got {tuple(modulation.shape)}")
+    return {name: modulation[:, i * hidden:(i + 1) * hidden] for i, name in enumerate(MODULATION_COLUMNS)}
+
+
+def _token_index(index: torch.Tensor, x: torch.Tensor, table_rows: int, check: bool) -> torch.Tensor:
+    """The per-token row index as the kernels take it: int64 [B, S]. Accepts
+    [S] (B == 1) or [B, S], int32 or int64 (the dtypes the reference accepts,
+    patches/InfiniLM.patch:1772-1775). With `check`, an index outside
+    [0, table_rows) raises (one device-to-host read of its min and max), as the
+    reference's narrow of the modulation row would."""
+    if index.device != x.device:
+        raise ValueError(f"index must be on {x.device}, got {index.device}")
+    if index.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"AdaLN indices must be int32 or int64, got {index.dtype}")
+    if index.dim() == 1 and x.shape[0] == 1:
+        index = index.unsqueeze(0)
+    if tuple(index.shape) != tuple(x.shape[:2]):
+        raise ValueError(f"index must be [B, S] = {tuple(x.shape[:2])} (or [S] for B == 1), got "
+                         f"{tuple(index.shape)}")
+    if index.dtype != torch.int64:
+        index = index.to(torch.int64)
+    if check and index.numel() > 0:
+        lo, hi = (int(v) for v in torch.aminmax(index))
+        if lo < 0 or hi >= table_rows:
+            raise ValueError(f"AdaLN index out of range: [{lo}, {hi}] not within [0, {table_rows})")
+    return index
+
+
+def make_rms_modulate_indexed(check_indices: bool = True):
+    """RMSNorm + AdaLN over [B, S, W] with scale/shift rows index[b, s] of [R, W]
+    tables: one launch for every segment of the indices. Returns
+    kernel(x, weight, eps, scale, shift, index, out). check_indices=False skips
+    the range check (no host synchronisation; out-of-range indices are clamped
+    by the kernel)."""
+
+    def kernel(x, weight, eps, scale, shift, index, out):
+        _ndim(3, x=x, out=out)
+        _ndim(2, scale=scale, shift=shift)
+        _ndim(1, weight=weight)
+        device = _bf16(x, weight, scale, shift, out)
+        index = _token_index(index, x, scale.shape[0], check_indices)
+        _lib.launch("launch_h3_rms_modulate_indexed", device, _lib.tensor(x), _lib.tensor(weight),
+                    _lib.scalar(eps), _lib.tensor(scale), _lib.tensor(shift), _lib.tensor(index),
+                    _lib.tensor(out))
+
+    return kernel
+
+
+def make_gated_residual_rms_modulate_indexed(check_indices: bool = True):
+    """residual = bf16(x + bf16(gate * y)); out = rms_modulate(residual), with
+    gate/scale/shift rows index[b, s] of [R, W] tables. Returns
+    kernel(x, gate, y, weight, eps, scale, shift, index, residual, out)."""
+
+    def kernel(x, gate, y, weight, eps, scale, shift, index, residual, out):
+        _ndim(3, x=x, y=y, residual=residual, out=out)
+        _ndim(2, gate=gate, scale=scale, shift=shift)
+        _ndim(1, weight=weight)
+        device = _bf16(x, gate, y, weight, scale, shift, residual, out)
+        index = _token_index(index, x, scale.shape[0], check_indices)
+        _lib.launch("launch_h3_gated_residual_rms_modulate_indexed", device, _lib.tensor(x), _lib.tensor(gate),
+                    _lib.tensor(y), _lib.tensor(weight), _lib.scalar(eps), _lib.tensor(scale),
+                    _lib.tensor(shift), _lib.tensor(index), _lib.tensor(residual), _lib.tensor(out))
+
+    return kernel
+
+
+def make_gated_residual_indexed(check_indices: bool = True):
+    """out = bf16(x + bf16(gate * y)) with the gate row index[b, s] of a [R, W]
+    table. Returns kernel(x, gate, y, index, out)."""
+
+    def kernel(x, gate, y, index, out):
+        _ndim(3, x=x, y=y, out=out)
+        _ndim(2, gate=gate)
+        device = _bf16(x, gate, y, out)
+        index = _token_index(index, x, gate.shape[0], check_indices)
+        _lib.launch("launch_h3_gated_residual_indexed", device, _lib.tensor(x), _lib.tensor(gate),
+                    _lib.tensor(y), _lib.tensor(index), _lib.tensor(out))
 
     return kernel
 

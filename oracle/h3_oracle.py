@@ -28,6 +28,12 @@ How each function is pinned (tests/test_oracle.py):
   / gated_residual_...      scale invariance (bitwise), fixed-order sum vs fp64
                             sum bound, float64 reference within 2 bf16 ulp,
                             scale=-1 and scale=0 modulation, fusion = unfused
+  adaln_segments            known answers (empty, one token, alternating,
+                            runs), coverage and maximality of the runs
+  *_segments / *_indexed    per-segment loops (the reference's call pattern)
+                            = per-token gather forms, bitwise, on random,
+                            alternating and single-row index patterns; a
+                            planted wrong row is detected
   rope_rotate_half          angle 0 = identity, angle pi/2 = exact rotation with
                             the i <-> i+48 pairing, pass-through bits, norm
   qk_norm_rope(_interleaved) = rms_norm(W=128) then the RoPE (composition),
@@ -157,6 +163,80 @@ def gated_residual_rms_modulate(x, gate, y, weight, eps, scale, shift, order="fi
     Returns (residual, out)."""
     residual = gated_residual(x, gate, y)
     return residual, rms_modulate(residual, weight, eps, scale, shift, order, eps_rounding)
+
+
+# ------------------------------------------------ AdaLN rows per token segment
+
+def adaln_segments(indices) -> list:
+    """Run-length segments (start, length, row) of the per-token AdaLN row
+    indices, in token order: a token extends the last segment when it names the
+    same row, else opens a new one (patches/InfiniLM.patch:1783-1790)."""
+    segments = []
+    for i, row in enumerate(torch.as_tensor(indices).reshape(-1).tolist()):
+        if segments and segments[-1][2] == row:
+            start, length, _ = segments[-1]
+            segments[-1] = (start, length + 1, row)
+        else:
+            segments.append((i, 1, row))
+    return segments
+
+
+def _segment_rows(x, segments):
+    """(rows of x [1, T, W] of each segment, the segment's table row)."""
+    if x.shape[0] != 1:
+        raise ValueError("the segmented forms take x [1, T, W], as the reference's hidden states")
+    for start, length, row in segments:
+        yield slice(start, start + length), row
+
+
+def rms_modulate_segments(x, weight, eps, scale_table, shift_table, segments):
+    """H3RMSModulate once per segment on the segment's rows, scale/shift the
+    segment's table row broadcast over them (patches/InfiniLM.patch:1376-1381,
+    the broadcast views of :1359-1364). x [1, T, W]; tables [R, W]."""
+    out = torch.empty_like(x)
+    for rows, row in _segment_rows(x, segments):
+        part = x[:, rows]
+        out[:, rows] = rms_modulate(part, weight, eps, scale_table[row].expand_as(part),
+                                    shift_table[row].expand_as(part))
+    return out
+
+
+def gated_residual_rms_modulate_segments(x, gate_table, y, weight, eps, scale_table, shift_table, segments):
+    """H3GatedResidualRMSModulate once per segment (patches/InfiniLM.patch:1384-1390).
+    Returns (residual, out)."""
+    residual, out = torch.empty_like(x), torch.empty_like(x)
+    for rows, row in _segment_rows(x, segments):
+        part = x[:, rows]
+        residual[:, rows], out[:, rows] = gated_residual_rms_modulate(
+            part, gate_table[row].expand_as(part), y[:, rows], weight, eps, scale_table[row].expand_as(part),
+            shift_table[row].expand_as(part))
+    return residual, out
+
+
+def gated_residual_segments(x, gate_table, y, segments):
+    """H3GatedResidual once per segment (patches/InfiniLM.patch:1392-1395)."""
+    out = torch.empty_like(x)
+    for rows, row in _segment_rows(x, segments):
+        part = x[:, rows]
+        out[:, rows] = gated_residual(part, gate_table[row].expand_as(part), y[:, rows])
+    return out
+
+
+def rms_modulate_indexed(x, weight, eps, scale_table, shift_table, index):
+    """The per-token form: token (b, s) takes row index[b, s] of the tables
+    (x [B, S, W], index [B, S], tables [R, W])."""
+    return rms_modulate(x, weight, eps, scale_table[index], shift_table[index])
+
+
+def gated_residual_rms_modulate_indexed(x, gate_table, y, weight, eps, scale_table, shift_table, index):
+    """Per-token form of gated_residual_rms_modulate_segments. Returns (residual, out)."""
+    return gated_residual_rms_modulate(x, gate_table[index], y, weight, eps, scale_table[index],
+                                       shift_table[index])
+
+
+def gated_residual_indexed(x, gate_table, y, index):
+    """Per-token form of gated_residual_segments."""
+    return gated_residual(x, gate_table[index], y)
 
 
 def swiglu(up: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:

@@ -95,6 +95,26 @@ CASES = [
      [t([1, 4, 128]), t([1, 4, 128]), t([1, 4, 128]), t([128]), scal(), t([1, 4, 128]), t([1, 4, 128]),
       t([1, 4, 127]), t([1, 4, 128])], "residual shape"),
     ("launch_h3_swiglu_exact", [t([1, 4, 128]), t([1, 4, 256]), t([1, 4, 128])], "gate shape"),
+    ("launch_h3_rms_modulate_indexed", [t([1, 4, 128]), t([128]), scal(), t([3, 128]), t([3, 128]), t([1, 5]),
+                                        t([1, 4, 128])], "index shape"),
+    ("launch_h3_rms_modulate_indexed", [t([1, 4, 128]), t([128]), scal(), t([3, 64]), t([3, 64]), t([1, 4]),
+                                        t([1, 4, 128])], "table width"),
+    ("launch_h3_rms_modulate_indexed", [t([1, 4, 128]), t([128]), scal(), t([3, 128]), t([2, 128]), t([1, 4]),
+                                        t([1, 4, 128])], "tables of different row counts"),
+    ("launch_h3_rms_modulate_indexed", [t([1, 4, 128]), t([128]), scal(), t([0, 128]), t([0, 128]), t([1, 4]),
+                                        t([1, 4, 128])], "empty tables"),
+    ("launch_h3_rms_modulate_indexed", [t([1, 4, 128]), t([128]), scal(), t([3, 128]), t([3, 128]), NULLSHAPE,
+                                        t([1, 4, 128])], "index without shape"),
+    ("launch_h3_gated_residual_rms_modulate_indexed",
+     [t([1, 4, 128]), t([2, 128]), t([1, 4, 128]), t([128]), scal(), t([3, 128]), t([3, 128]), t([1, 4]),
+      t([1, 4, 128]), t([1, 4, 128])], "gate table rows"),
+    ("launch_h3_gated_residual_rms_modulate_indexed",
+     [t([1, 4, 128]), t([3, 128]), t([1, 4, 128]), t([128]), scal(), t([3, 128]), t([3, 128]), t([4, 1]),
+      t([1, 4, 128]), t([1, 4, 128])], "index transposed"),
+    ("launch_h3_gated_residual_indexed", [t([1, 4, 128]), t([1, 4, 128]), t([1, 4, 128]), t([1, 4]),
+                                          t([1, 4, 128])], "3-D gate on the indexed kernel"),
+    ("launch_h3_gated_residual_indexed", [t([1, 4, 128]), t([0, 128]), t([1, 4, 128]), t([1, 4]),
+                                          t([1, 4, 128])], "empty gate table"),
     ("launch_h3_rope_exact", [t([4, 2, 128]), t([4, 2, 128], data=ADDR + 256), t([4, 2, 128]), t([4, 48]),
                               t([4, 48]), t([4, 2, 128]), t([4, 2, 128]), t([4, 2, 128])], "unaliased x views"),
     ("launch_h3_rope_exact", [t([4, 2, 128])] * 3 + [t([4, 64]), t([4, 64])] + [t([4, 2, 128])] * 3, "table 64"),
@@ -139,6 +159,12 @@ EMPTY = [
                                       t([0, 4, 128])]),
     ("launch_h3_gated_residual_exact", [t([1, 0, 64])] * 4),
     ("launch_h3_swiglu_exact", [t([1, 4, 0])] * 3),
+    ("launch_h3_rms_modulate_indexed", [t([1, 0, 128]), t([128]), scal(), t([0, 128]), t([0, 128]), t([1, 0]),
+                                        t([1, 0, 128])]),
+    ("launch_h3_gated_residual_rms_modulate_indexed",
+     [t([1, 0, 128]), t([2, 128]), t([1, 0, 128]), t([128]), scal(), t([2, 128]), t([2, 128]), t([1, 0]),
+      t([1, 0, 128]), t([1, 0, 128])]),
+    ("launch_h3_gated_residual_indexed", [t([1, 0, 64]), t([2, 64]), t([1, 0, 64]), t([1, 0]), t([1, 0, 64])]),
     ("launch_h3_qk_norm_rope", [t([0, 1, 2, 128])] * 3 + [t([128])] * 3 + [scal(), t([0, 48]), t([0, 48])]
      + [t([0, 1, 2, 128])] * 3),
     ("launch_h3_rope_cache", [t([0, 3]), t([16]), t([0, 48]), t([0, 48])]),
