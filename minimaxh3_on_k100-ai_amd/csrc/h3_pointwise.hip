@@ -123,13 +123,24 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 // (b, s) itself, or (index[b, s], 0) in the tables (a table is a Rows view with
 // its row stride in sb), the index clamped into [0, count) so that no value
 // of it reads outside the tables.
+__device__ __forceinline__ int64_t index_row(const ModIndex &ix, int64_t b, int64_t s) {
+    const int64_t m = ix.p[b * ix.sb + s * ix.ss];
+    return m < 0 ? 0 : (m < ix.count ? m : ix.count - 1);
+}
+// index_row for a (b, s) the whole wave shares, read with a scalar load (the
+// index is read-only for the kernel's lifetime): the value lands in scalar
+// registers, not in two vector registers per index.
+__device__ __forceinline__ int64_t index_row_uniform(const ModIndex &ix, int64_t b, int64_t s) {
+    typedef const __attribute__((address_space(4))) int64_t *ConstantPtr;
+    const int64_t m = *(ConstantPtr)(ix.p + b * ix.sb + s * ix.ss);
+    return m < 0 ? 0 : (m < ix.count ? m : ix.count - 1);
+}
 __device__ __forceinline__ void mod_coords(const ModIndex &ix, int64_t b, int64_t s, int64_t &mb, int64_t &ms) {
     if (ix.p == nullptr) {
         mb = b;
         ms = s;
     } else {
-        const int64_t m = ix.p[b * ix.sb + s * ix.ss];
-        mb = m < 0 ? 0 : (m < ix.count ? m : ix.count - 1);
+        mb = index_row(ix, b, s);
         ms = 0;
     }
 }
@@ -438,6 +449,114 @@ __global__ __launch_bounds__(THREADS) void rms_staged_kernel(RmsArgs a) {
     }
 }
 
+// RMSNorm + AdaLN with per-token modulation rows (ModIndex), W8 <= 64 * G:
+// rms_staged_kernel's order and register use over all B * S rows. A block
+// takes groups of kWaves consecutive rows, one per wave, the groups
+// grid-strided. The weight is staged once. Every wave reads all kWaves
+// indices of its group (the same values, so every wave takes the same
+// branches below): when they name one table row -- nearly every group, the
+// indices coming in long runs -- that row's factor and shift are staged in LDS
+// unless they are there already; a group across a run boundary reads each
+// row's factor and shift from the tables (L2) instead. The launch bound keeps
+// two blocks resident per CU up to G = 14 (W = 7168).
+template <int G, int THREADS>
+__global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed_kernel(RmsArgs a) {
+    constexpr int kWaves = THREADS / 64;
+    extern __shared__ U4 staged[];
+    const int W8 = (a.W + 7) / 8;
+    U4 *lw = staged, *lk = staged + W8, *lsh = staged + 2 * W8;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kWaves;
+    const int64_t last = a.rows - 1;
+    U4 v[G];
+    auto load_row = [&](int64_t b, int64_t s) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[k] = ld16_stream(row_ptr(a.x, b, s) + clamp_group(lane + 64 * k, W8) * 8);
+        __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
+    };
+    int64_t in_lds = -1;
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWaves; base < a.rows; base += step) {
+        // same trip count in every wave
+        const bool ok = base + wave < a.rows;
+        // Coordinates of the group's rows (rows past the end repeat the last
+        // row), walked from one division. The wave's own row is loaded first,
+        // then the group's indices, whose wait overlaps the row's; no load
+        // sits under a branch, which would wait for it at the branch's end.
+        int64_t bw[kWaves], sw[kWaves], m[kWaves], b = 0, s = 0;
+        {
+            const int64_t i0 = base < last ? base : last;
+            bw[0] = i0 / a.S;
+            sw[0] = i0 % a.S;
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) {
+                const bool wrap = base + w <= last && sw[w - 1] + 1 == a.S;
+                bw[w] = wrap ? bw[w - 1] + 1 : bw[w - 1];
+                sw[w] = wrap ? 0 : (base + w <= last ? sw[w - 1] + 1 : sw[w - 1]);
+            }
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                b = w == wave ? bw[w] : b;
+                s = w == wave ? sw[w] : s;
+            }
+        }
+        load_row(b, s);
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) m[w] = index_row_uniform(a.index, bw[w], sw[w]);
+        int64_t mine = m[0];
+        bool same = true;
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            mine = w == wave ? m[w] : mine;
+            same = same && m[w] == m[0];
+        }
+        // Staging: the weight with the first group, the group's table row when
+        // it changes. The loads go out while the row's own are in flight.
+        const bool first = base == static_cast<int64_t>(blockIdx.x) * kWaves;
+        const bool restage = same && m[0] != in_lds;
+        if (first || restage) {
+            if (!first) __syncthreads();  // the earlier groups' reads of the staged rows are done
+            for (int g = threadIdx.x; g < W8; g += THREADS) {
+                if (first) lw[g] = ld16(a.w + g * 8);
+                if (restage) {
+                    lk[g] = factor_of(ld16(row_ptr(a.scale, m[0], 0) + g * 8));
+                    lsh[g] = ld16(row_ptr(a.shift, m[0], 0) + g * 8);
+                }
+            }
+            __syncthreads();
+            in_lds = restage ? m[0] : in_lds;
+        }
+        float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const U4 unused{};
+            v[k] = rms_phase1<kRmsModulate>(v[k], unused, unused, lane + 64 * k < W8, part[k & 3]);
+            keep_packed(v[k]);
+        }
+        const float total = (fold_lanes<64>(part[0]) + fold_lanes<64>(part[2])) +
+                            (fold_lanes<64>(part[1]) + fold_lanes<64>(part[3]));
+        const float r = rms_reciprocal(total, a.W, a.eps_bf);
+        if (same) {
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                const int g = lane + 64 * k, gc = clamp_group(g, W8);
+                const U4 o = rms_phase2<kRmsModulate>(v[k], r, lw[gc], lk[gc], lsh[gc]);
+                if (ok && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                const int g = lane + 64 * k, gc = clamp_group(g, W8);
+                const U4 kv = factor_of(ld16(row_ptr(a.scale, mine, 0) + gc * 8));
+                const U4 shv = ld16(row_ptr(a.shift, mine, 0) + gc * 8);
+                const U4 o = rms_phase2<kRmsModulate>(v[k], r, lw[gc], kv, shv);
+                if (ok && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+                __builtin_amdgcn_sched_barrier(0);  // one group's table loads at a time (registers)
+            }
+        }
+    }
+}
+
 // Rows whose weight, modulation and gate vectors are the same for every s of
 // a batch entry b: one row at a time per 256-thread block, thread t owning
 // groups t, t + 256, ... (the fixed order itself). The block stages the
@@ -618,6 +737,20 @@ int launch_rms_vec(const RmsArgs &a, hipStream_t stream) {
         // Per-token modulation rows: rms_stream_kernel over all rows, restaging
         // the tables' row at each change of index.
         const int vpt = (W8 + kThreads - 1) / kThreads;
+        if (MODE == kRmsModulate && a.index.p != nullptr && lds <= 65536 && need <= 16) {
+            constexpr int kWaves = kStagedThreads / 64;
+            const int64_t groups = (a.rows + kWaves - 1) / kWaves;
+            const unsigned grid = static_cast<unsigned>(groups < kStagedBlocks ? groups : kStagedBlocks);
+#define H3_RMS_MOD_INDEXED(GG)                                                                              \
+    if (need <= GG) {                                                                                      \
+        rms_modulate_indexed_kernel<GG, kStagedThreads><<<grid, kStagedThreads, lds, stream>>>(a);         \
+        return launch_status();                                                                            \
+    }
+            H3_RMS_MOD_INDEXED(2) H3_RMS_MOD_INDEXED(3) H3_RMS_MOD_INDEXED(4) H3_RMS_MOD_INDEXED(6)
+            H3_RMS_MOD_INDEXED(8) H3_RMS_MOD_INDEXED(10) H3_RMS_MOD_INDEXED(12) H3_RMS_MOD_INDEXED(14)
+            H3_RMS_MOD_INDEXED(16)
+#undef H3_RMS_MOD_INDEXED
+        }
         if (a.index.p != nullptr && lds <= 65536 && vpt <= 4) {
             const unsigned grid = static_cast<unsigned>(a.rows < kStreamBlocks ? a.rows : kStreamBlocks);
 #define H3_RMS_STREAM_INDEXED(V)                                                            \
