@@ -130,6 +130,18 @@ def bench_pointwise(pkg, device) -> dict:
     ms = time_graph([lambda x=x, o=o: k_rh(x, w, 1e-6, table48[:, :48], table48[:, 48:], o) for x, o in zip(xs, outs)])
     record("qk_norm_rope", ms, nbytes, [T, 1, H, 128])
     del xs, outs
+    # q, k and v of one head group in one launch: by-rank views of the fused
+    # [T, 3, H, 128] projection in, [1, T, H, 128] send buffers out, RoPE cache
+    # rows gathered by a permutation of the positions.
+    projs = [rnd(T, 3, H, 128) for _ in range(3)]
+    sends = [torch.empty(3, 1, T, H, 128, dtype=bf, device=device) for _ in range(3)]
+    views = [(pkg.qkv_by_rank(p, 1), [s[i].permute(1, 0, 2, 3) for i in range(3)]) for p, s in zip(projs, sends)]
+    positions = torch.randperm(T, device=device)
+    k_pack = pkg.make_qkv_norm_rope_pack()
+    nbytes = 6 * T * H * 128 * 2 + T * 8 + T * 96 * 2 + 2 * 128 * 2
+    ms = time_graph([lambda i=i, o=o: k_pack(*i, w, w, 1e-6, table48, positions, *o) for i, o in views])
+    record("qkv_norm_rope_pack", ms, nbytes, [T, 1, H, 128])
+    del projs, sends, views
 
     S, C, F = 8192, 7168, 18432
     rot = 3

@@ -213,6 +213,31 @@ NineToothedResult launch_h3_qk_norm_rope(NineToothedStream stream, NineToothedTe
                                          NineToothedTensor y0, NineToothedTensor y1,
                                          NineToothedTensor yp);
 
+/* The q, k and v head rows of one head group in ONE launch, in the layout of
+ * the reference's sequence-parallel attention (patches/InfiniLM.patch:1071-1110):
+ * q and k get launch_h3_qk_norm_rope's per-head RMSNorm + rotate-half RoPE,
+ * with their cos/sin rows gathered from the RoPE cache through the token
+ * positions, and v is copied.
+ *   q, k, v: bf16 [T, P, Hs, 128], any strides (the by-rank views of the fused
+ *     [T, 3, P * Hs, 128] projection, :1093-1097);
+ *   q_out, k_out, v_out: bf16 [T, P, Hs, 128], any strides (the permuted
+ *     [P, T, Hs, 128] all-to-all send buffers, :1098-1102);
+ *   q_weight, k_weight: bf16 [128]; eps: fp64 scalar;
+ *   cos, sin: bf16 [N, 48], the halves of the [N, 96] RoPE cache;
+ *   positions: int64 [T], token t's row of the cache (a value outside
+ *     [0, N) is clamped into it; the kernel never reads outside the cache).
+ * Per-step bf16 rounding as launch_h3_qk_norm_rope; v is copied bit for bit.
+ * Replaces, per head group, the gather_rows of the cache (:1077-1080), the two
+ * launch_h3_qk_norm_rope calls (:1098-1102, via patches/InfiniCore.patch:1180-1182)
+ * and the v send-block copy (:1063-1069,1104). */
+NineToothedResult launch_h3_qkv_norm_rope_pack(NineToothedStream stream, NineToothedTensor q,
+                                               NineToothedTensor k, NineToothedTensor v,
+                                               NineToothedTensor q_weight, NineToothedTensor k_weight,
+                                               NineToothedTensor eps, NineToothedTensor cos,
+                                               NineToothedTensor sin, NineToothedTensor positions,
+                                               NineToothedTensor q_out, NineToothedTensor k_out,
+                                               NineToothedTensor v_out);
+
 /* The same RMSNorm followed by an interleaved-pair RoPE over all 128
  * channels: pair i = channels (2i, 2i+1), angle table cos/sin [T, 64]
  * (rotary channels split 32/48/48 over the t/h/w axes). Per-step bf16

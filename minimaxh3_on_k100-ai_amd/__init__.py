@@ -21,6 +21,7 @@ from .h3_pointwise import (  # noqa: F401
     make_gated_residual_rms_modulate_indexed,
     make_qk_norm_rope,
     make_qk_norm_rope_interleaved,
+    make_qkv_norm_rope_pack,
     make_rms,
     make_rms_modulate,
     make_rms_modulate_indexed,
@@ -28,6 +29,7 @@ from .h3_pointwise import (  # noqa: F401
     make_rope_cache,
     make_swiglu,
     modulation_columns,
+    qkv_by_rank,
 )
 
 library = _lib.library

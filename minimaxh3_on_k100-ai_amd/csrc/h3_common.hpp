@@ -79,6 +79,38 @@ inline bool rows_vec16(const View<N> &v, int elem) {
     return true;
 }
 
+// True when every element offset of the view is a non-negative value below
+// 2^31, so that kernels may form it in 32-bit arithmetic.
+template <int N>
+inline bool offsets_fit_int32(const View<N> &v) {
+    int64_t span = 0;
+    for (int i = 0; i < N; ++i) {
+        if (v.shape[i] == 0) return true;
+        if (v.stride[i] < 0 || v.stride[i] >= (int64_t{1} << 31)) return false;
+        span += v.stride[i] * (v.shape[i] - 1);
+    }
+    return span < (int64_t{1} << 31);
+}
+
+// Division by a divisor fixed at launch, for dividends n < 2^31: q = floor(n / d)
+// = (n * m) >> shift with m = ceil(2^(31 + s) / d), s = ceil(log2 d). The error
+// of m is below 1, so n * m / 2^(31 + s) exceeds n / d by less than
+// n / 2^(31 + s) < 2^-s <= 1 / d, which never reaches the next integer.
+struct FastDiv {
+    uint32_t d, m, shift;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((uint64_t{1} << s) < d) ++s;
+    const uint64_t m = ((uint64_t{1} << (31 + s)) + d - 1) / d;
+    return {d, static_cast<uint32_t>(m), 31 + s};
+}
+
+__host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> f.shift);
+}
+
 inline hipStream_t as_stream(NineToothedStream s) { return static_cast<hipStream_t>(s); }
 
 // Launch epilogue shared by all launchers: the launch status of the kernel.

@@ -1102,6 +1102,7 @@ struct RopeArgs {
     const bf16_t *cos, *sin;
     int64_t cs0, cs1, ss0, ss1;  // element strides of the [T, n] cos and sin tables
     int64_t rows, P, Hs;
+    FastDiv by_ph, by_h;  // row -> (t, p, h): divisions by P * Hs and by Hs
     const bf16_t *w;  // [128] RMS weight (norm kernels only)
     int64_t w_stride;
     float eps_bf;
@@ -1109,8 +1110,25 @@ struct RopeArgs {
 
 enum RopeMode { kRopeOnly = 0, kNormRope = 1, kNormRopeInterleaved = 2 };
 
-__device__ __forceinline__ int64_t head_offset(const HeadRows &h, int64_t t, int64_t p, int64_t hh) {
-    return t * h.s0 + p * h.s1 + hh * h.s2;
+// Element offset of head row (t, p, hh); OFF32 when the host has checked that
+// every offset of the view is below 2^31 (offsets_fit_int32).
+template <bool OFF32>
+__device__ __forceinline__ int64_t head_offset(const HeadRows &h, uint32_t t, uint32_t p, uint32_t hh) {
+    if constexpr (OFF32) {
+        return static_cast<int64_t>(t * static_cast<uint32_t>(h.s0) + p * static_cast<uint32_t>(h.s1) +
+                                    hh * static_cast<uint32_t>(h.s2));
+    } else {
+        return static_cast<int64_t>(t) * h.s0 + static_cast<int64_t>(p) * h.s1 + static_cast<int64_t>(hh) * h.s2;
+    }
+}
+
+// Row r of the [T, P, Hs] row space -> (t, p, hh), r < 2^31.
+__device__ __forceinline__ void split_row(uint32_t r, const FastDiv &by_ph, const FastDiv &by_h, uint32_t &t,
+                                          uint32_t &p, uint32_t &hh) {
+    t = fast_div(r, by_ph);
+    const uint32_t rem = r - t * by_ph.d;
+    p = fast_div(rem, by_h);
+    hh = rem - p * by_h.d;
 }
 
 template <bool VEC>
@@ -1130,11 +1148,13 @@ struct RopeTab {
     U4 c, s;
 };
 
-template <bool VEC, int MODE>
-__device__ __forceinline__ RopeTab load_tab(const RopeArgs &a, int64_t t, int lane) {
+template <bool VEC, int MODE, bool OFF32>
+__device__ __forceinline__ RopeTab load_tab(const RopeArgs &a, uint32_t t, int lane) {
     RopeTab tab{};
-    const bf16_t *cr = a.cos + t * a.cs0;
-    const bf16_t *sr = a.sin + t * a.ss0;
+    const bf16_t *cr = a.cos + (OFF32 ? static_cast<int64_t>(t * static_cast<uint32_t>(a.cs0))
+                                      : static_cast<int64_t>(t) * a.cs0);
+    const bf16_t *sr = a.sin + (OFF32 ? static_cast<int64_t>(t * static_cast<uint32_t>(a.ss0))
+                                      : static_cast<int64_t>(t) * a.ss0);
     if constexpr (MODE == kNormRopeInterleaved) {
         const int c0 = lane * 4;
         if constexpr (VEC) {
@@ -1230,26 +1250,24 @@ __device__ __forceinline__ void rope_interleaved(float f[8], const RopeTab &tab)
 
 // R rows per 16-lane group: every row's x and table loads are issued before
 // the arithmetic of the first.
-template <bool VEC, int MODE, int R>
+template <bool VEC, int MODE, int R, bool OFF32>
 __global__ __launch_bounds__(kThreads) void head_rows_kernel(RopeArgs a) {
     constexpr int kGroups = kThreads / 16;
     const int lane = threadIdx.x & 15;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kGroups * R + (threadIdx.x >> 4);
+    const uint32_t base = blockIdx.x * kGroups * R + (threadIdx.x >> 4);  // rows < 2^31 (host check)
     bool ok[R];
     int64_t out_off[R];
     U4 xv[R];
     RopeTab tab[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int64_t row = base + r * kGroups;
+        const uint32_t row = base + r * kGroups;
         ok[r] = row < a.rows;
-        const int64_t rr = ok[r] ? row : 0;
-        const int64_t t = rr / (a.P * a.Hs);
-        const int64_t rem = rr % (a.P * a.Hs);
-        const int64_t p = rem / a.Hs, hh = rem % a.Hs;
-        out_off[r] = head_offset(a.out, t, p, hh);
-        xv[r] = load_head<VEC>(a.x, head_offset(a.x, t, p, hh), lane);
-        tab[r] = load_tab<VEC, MODE>(a, t, lane);
+        uint32_t t, p, hh;
+        split_row(ok[r] ? row : 0u, a.by_ph, a.by_h, t, p, hh);
+        out_off[r] = head_offset<OFF32>(a.out, t, p, hh);
+        xv[r] = load_head<VEC>(a.x, head_offset<OFF32>(a.x, t, p, hh), lane);
+        tab[r] = load_tab<VEC, MODE, OFF32>(a, t, lane);
     }
     float w[8];
     if constexpr (MODE != kRopeOnly) u4_to_f8(load_group<VEC>(a.w, a.w_stride, lane * 8, 128), w);
@@ -1288,6 +1306,11 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
     a.P = x.shape[1];
     a.Hs = x.shape[2];
     a.rows = x.shape[0] * x.shape[1] * x.shape[2];
+    if (a.rows >= (int64_t{1} << 31) - kThreads * 4) return kInvalid;
+    a.by_ph = make_fastdiv(static_cast<uint32_t>(a.P * a.Hs > 0 ? a.P * a.Hs : 1));
+    a.by_h = make_fastdiv(static_cast<uint32_t>(a.Hs > 0 ? a.Hs : 1));
+    const bool off32 = offsets_fit_int32(x) && offsets_fit_int32(out) && offsets_fit_int32(cos) &&
+                       offsets_fit_int32(sin);
     if (w != nullptr) {
         a.w = reinterpret_cast<const bf16_t *>(w->data);
         a.w_stride = w->stride[0];
@@ -1301,17 +1324,159 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
     const int64_t grid = (a.rows + per_block - 1) / per_block;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     const unsigned g = static_cast<unsigned>(grid);
-    if (vec) {
-        if (four)
-            head_rows_kernel<true, MODE, 4><<<g, kThreads, 0, stream>>>(a);
-        else
-            head_rows_kernel<true, MODE, 1><<<g, kThreads, 0, stream>>>(a);
-    } else {
-        if (four)
-            head_rows_kernel<false, MODE, 4><<<g, kThreads, 0, stream>>>(a);
-        else
-            head_rows_kernel<false, MODE, 1><<<g, kThreads, 0, stream>>>(a);
+#define H3_HEAD_ROWS(V, R, O) \
+    if (vec == V && (four ? 4 : 1) == R && off32 == O) head_rows_kernel<V, MODE, R, O><<<g, kThreads, 0, stream>>>(a);
+    H3_HEAD_ROWS(true, 4, true) H3_HEAD_ROWS(true, 1, true) H3_HEAD_ROWS(true, 4, false)
+    H3_HEAD_ROWS(true, 1, false) H3_HEAD_ROWS(false, 4, true) H3_HEAD_ROWS(false, 1, true)
+    H3_HEAD_ROWS(false, 4, false) H3_HEAD_ROWS(false, 1, false)
+#undef H3_HEAD_ROWS
+    return launch_status();
+}
+
+// ============================================================ q/k/v send pack
+
+// One launch over the q, k and v head rows of a head group as InfiniLM's
+// sequence-parallel attention produces them (patches/InfiniLM.patch:1071-1110):
+// q and k get the per-head RMSNorm + rotate-half RoPE of head_rows_kernel, with
+// the cos/sin rows gathered from the RoPE cache through the token positions
+// (the gather_rows of :1077-1080, fused), and v is copied; every input and
+// output is a [T, P, Hs, 128] view with any strides (the by-rank views of the
+// fused projection, :1093-1097, and the permuted send buffers, :1100-1102).
+struct QkvArgs {
+    HeadRows q, k, v, q_out, k_out, v_out;
+    const bf16_t *wq, *wk;
+    int64_t wq_stride, wk_stride;
+    const bf16_t *cos, *sin;
+    int64_t cs0, cs1, ss0, ss1;
+    const int64_t *pos;
+    int64_t pos_stride, table_rows;
+    int64_t rows, P, Hs;  // rows = T * P * Hs per tensor
+    FastDiv by_ph, by_h;
+    float eps_bf;
+};
+
+__device__ __forceinline__ HeadRows pick3(int kind, const HeadRows &a, const HeadRows &b, const HeadRows &c) {
+    // Field by field, so that the choice stays in scalar registers.
+    return {kind == 0 ? a.p : (kind == 1 ? b.p : c.p), kind == 0 ? a.s0 : (kind == 1 ? b.s0 : c.s0),
+            kind == 0 ? a.s1 : (kind == 1 ? b.s1 : c.s1), kind == 0 ? a.s2 : (kind == 1 ? b.s2 : c.s2),
+            kind == 0 ? a.s3 : (kind == 1 ? b.s3 : c.s3)};
+}
+
+// Block b handles tensor b % 3 (0 q, 1 k, 2 v) and R rows per 16-lane group
+// of tile b / 3. Every load (x, position, table, weight) is issued for every
+// block kind from valid addresses; the kind only selects the arithmetic.
+template <bool VEC, int R, bool OFF32>
+__global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
+    constexpr int kGroups = kThreads / 16;
+    const int kind = static_cast<int>(blockIdx.x % 3);
+    const int64_t tile = blockIdx.x / 3;
+    const int lane = threadIdx.x & 15;
+    const HeadRows in = pick3(kind, a.q, a.k, a.v), out = pick3(kind, a.q_out, a.k_out, a.v_out);
+    const uint32_t base = static_cast<uint32_t>(tile) * kGroups * R + (threadIdx.x >> 4);
+    bool ok[R];
+    int64_t out_off[R];
+    uint32_t t[R];
+    U4 xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = base + r * kGroups;
+        ok[r] = row < a.rows;
+        uint32_t p, hh;
+        split_row(ok[r] ? row : 0u, a.by_ph, a.by_h, t[r], p, hh);
+        out_off[r] = head_offset<OFF32>(out, t[r], p, hh);
+        xv[r] = load_head<VEC>(in, head_offset<OFF32>(in, t[r], p, hh), lane);
     }
+    uint32_t trow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t m = a.pos[OFF32 ? static_cast<int64_t>(t[r] * static_cast<uint32_t>(a.pos_stride))
+                                       : static_cast<int64_t>(t[r]) * a.pos_stride];
+        trow[r] = static_cast<uint32_t>(m < 0 ? 0 : (m < a.table_rows ? m : a.table_rows - 1));
+    }
+    RopeTab tab[R];
+    RopeArgs ta{};
+    ta.cos = a.cos;
+    ta.sin = a.sin;
+    ta.cs0 = a.cs0;
+    ta.cs1 = a.cs1;
+    ta.ss0 = a.ss0;
+    ta.ss1 = a.ss1;
+#pragma unroll
+    for (int r = 0; r < R; ++r) tab[r] = load_tab<VEC, kNormRope, OFF32>(ta, trow[r], lane);
+    float w[8];
+    u4_to_f8(load_group<VEC>(kind == 0 ? a.wq : a.wk, kind == 0 ? a.wq_stride : a.wk_stride, lane * 8, 128), w);
+    if (kind == 2) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (ok[r]) store_group<VEC, true>(reinterpret_cast<bf16_t *>(out.p) + out_off[r], out.s3, lane * 8, 128, xv[r]);
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float f[8];
+        u4_to_f8(xv[r], f);
+        head_rms(f, w, a.eps_bf);
+        rope_rotate_half(f, lane, tab[r]);
+        if (ok[r]) store_head<VEC>(out, out_off[r], lane, f);
+    }
+}
+
+int launch_qkv_pack(hipStream_t stream, const View<4> *in, const View<4> *out, const View<1> &wq,
+                    const View<1> &wk, double eps, const View<2> &cos, const View<2> &sin,
+                    const View<1> &pos) {
+    for (int i = 0; i < 3; ++i)
+        if (!same_shape(in[i], in[0]) || !same_shape(out[i], in[0])) return kInvalid;
+    if (in[0].shape[3] != 128 || wq.shape[0] != 128 || wk.shape[0] != 128) return kInvalid;
+    if (cos.shape[1] != 48 || !same_shape(cos, sin) || pos.shape[0] != in[0].shape[0]) return kInvalid;
+    const int64_t rows = in[0].shape[0] * in[0].shape[1] * in[0].shape[2];
+    if (rows != 0 && cos.shape[0] == 0) return kInvalid;  // no table row for the tokens to take
+    bool vec = rows_vec16(cos, 2) && rows_vec16(sin, 2) && rows_vec16(wq, 2) && rows_vec16(wk, 2);
+    for (int i = 0; i < 3; ++i) vec = vec && rows_vec16(in[i], 2) && rows_vec16(out[i], 2);
+    auto head_rows = [](const View<4> &v) {
+        return HeadRows{v.data, v.stride[0], v.stride[1], v.stride[2], v.stride[3]};
+    };
+    QkvArgs a{};
+    a.q = head_rows(in[0]);
+    a.k = head_rows(in[1]);
+    a.v = head_rows(in[2]);
+    a.q_out = head_rows(out[0]);
+    a.k_out = head_rows(out[1]);
+    a.v_out = head_rows(out[2]);
+    a.wq = reinterpret_cast<const bf16_t *>(wq.data);
+    a.wk = reinterpret_cast<const bf16_t *>(wk.data);
+    a.wq_stride = wq.stride[0];
+    a.wk_stride = wk.stride[0];
+    a.cos = reinterpret_cast<const bf16_t *>(cos.data);
+    a.sin = reinterpret_cast<const bf16_t *>(sin.data);
+    a.cs0 = cos.stride[0];
+    a.cs1 = cos.stride[1];
+    a.ss0 = sin.stride[0];
+    a.ss1 = sin.stride[1];
+    a.pos = reinterpret_cast<const int64_t *>(pos.data);
+    a.pos_stride = pos.stride[0];
+    a.table_rows = cos.shape[0];
+    a.rows = rows;
+    a.P = in[0].shape[1];
+    a.Hs = in[0].shape[2];
+    a.eps_bf = host_round_bf16(eps);
+    if (rows == 0) return 0;
+    if (rows >= (int64_t{1} << 31) - kThreads * 4) return kInvalid;
+    a.by_ph = make_fastdiv(static_cast<uint32_t>(a.P * a.Hs));
+    a.by_h = make_fastdiv(static_cast<uint32_t>(a.Hs));
+    bool off32 = offsets_fit_int32(cos) && offsets_fit_int32(sin) && offsets_fit_int32(pos);
+    for (int i = 0; i < 3; ++i) off32 = off32 && offsets_fit_int32(in[i]) && offsets_fit_int32(out[i]);
+    // Four rows per lane group when that still leaves >= 1024 blocks per tensor.
+    constexpr int64_t kPerBlock = kThreads / 16;
+    const bool four = (rows + 4 * kPerBlock - 1) / (4 * kPerBlock) >= 1024;
+    const int64_t per_block = four ? 4 * kPerBlock : kPerBlock;
+    const int64_t grid = 3 * ((rows + per_block - 1) / per_block);
+    if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
+    const unsigned g = static_cast<unsigned>(grid);
+#define H3_QKV(V, R, O) \
+    if (vec == V && (four ? 4 : 1) == R && off32 == O) qkv_pack_kernel<V, R, O><<<g, kThreads, 0, stream>>>(a);
+    H3_QKV(true, 4, true) H3_QKV(true, 1, true) H3_QKV(true, 4, false) H3_QKV(true, 1, false)
+    H3_QKV(false, 4, true) H3_QKV(false, 1, true) H3_QKV(false, 4, false) H3_QKV(false, 1, false)
+#undef H3_QKV
     return launch_status();
 }
 
@@ -1469,6 +1634,26 @@ NineToothedResult launch_h3_qk_norm_rope_interleaved(NineToothedStream stream, N
         !load_view(weight, 2, w) || !load_scalar(eps, e))
         return kInvalid;
     return launch_head_rows<kNormRopeInterleaved>(as_stream(stream), xv, o, c, s, &w, e);
+}
+
+NineToothedResult launch_h3_qkv_norm_rope_pack(NineToothedStream stream, NineToothedTensor q,
+                                               NineToothedTensor k, NineToothedTensor v,
+                                               NineToothedTensor q_weight, NineToothedTensor k_weight,
+                                               NineToothedTensor eps, NineToothedTensor cos,
+                                               NineToothedTensor sin, NineToothedTensor positions,
+                                               NineToothedTensor q_out, NineToothedTensor k_out,
+                                               NineToothedTensor v_out) {
+    View<4> in[3], out[3];
+    View<1> wq, wk, pos;
+    View<2> c, sn;
+    double e;
+    const NineToothedTensor ins[3] = {q, k, v}, outs[3] = {q_out, k_out, v_out};
+    for (int i = 0; i < 3; ++i)
+        if (!load_view(ins[i], 2, in[i]) || !load_view(outs[i], 2, out[i])) return kInvalid;
+    if (!load_view(q_weight, 2, wq) || !load_view(k_weight, 2, wk) || !load_scalar(eps, e) ||
+        !load_view(cos, 2, c) || !load_view(sin, 2, sn) || !load_view(positions, 8, pos))
+        return kInvalid;
+    return launch_qkv_pack(as_stream(stream), in, out, wq, wk, e, c, sn, pos);
 }
 
 NineToothedResult launch_h3_rope_cache(NineToothedStream stream, NineToothedTensor position,

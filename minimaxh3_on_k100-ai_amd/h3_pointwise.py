@@ -18,7 +18,8 @@ __all__ = [
     "make_swiglu", "make_rms", "make_rms_modulate", "make_gated_residual",
     "make_gated_residual_rms_modulate", "make_rope", "make_qk_norm_rope",
     "make_qk_norm_rope_interleaved", "make_rope_cache", "modulation_columns", "make_rms_modulate_indexed",
-    "make_gated_residual_rms_modulate_indexed", "make_gated_residual_indexed",
+    "make_gated_residual_rms_modulate_indexed", "make_gated_residual_indexed", "qkv_by_rank",
+    "make_qkv_norm_rope_pack",
 ]
 
 
@@ -257,6 +258,51 @@ def make_qk_norm_rope(caller="torch", output_dir=None, archs=None, rows=8, num_w
         _qk_raw(x, x, x, weight, weight, weight, eps, cos, sin, out, out, out)
 
     return launch
+
+
+def qkv_by_rank(projected: torch.Tensor, ranks: int):
+    """The q, k and v parts of the fused projection [T, 3, P * Hs, 128] as
+    [T, P, Hs, 128] views by destination rank, as InfiniLM builds them
+    (patches/InfiniLM.patch:1089-1097). Views, no copies."""
+    if projected.dim() != 4 or projected.shape[1] != 3 or projected.shape[2] % ranks != 0:
+        raise ValueError(f"projected must be [T, 3, P * Hs, D] with P = {ranks}, got {tuple(projected.shape)}")
+    T, _, width, D = projected.shape
+    hs = width // ranks
+    parts = []
+    for i in range(3):
+        part = projected[:, i]
+        s0, s1, s2 = part.stride()
+        parts.append(part.as_strided((T, ranks, hs, D), (s0, hs * s1, s1, s2)))
+    return tuple(parts)
+
+
+def make_qkv_norm_rope_pack(dtype=None):
+    """q/k per-head RMSNorm + rotate-half RoPE and the v copy of one head group
+    in one launch, cos/sin rows gathered from the [N, 96] RoPE cache through the
+    token positions (patches/InfiniLM.patch:1071-1110). Returns
+    kernel(q, k, v, q_weight, k_weight, eps, cache, positions, q_out, k_out, v_out):
+    q, k, v and the outputs [T, P, Hs, 128] with any strides (see qkv_by_rank;
+    the outputs are typically send buffers [P, T, Hs, 128] permuted to
+    [T, P, Hs, 128]); positions int64 [T] (int32 is widened)."""
+    _bf16_only(dtype)
+
+    def kernel(q, k, v, q_weight, k_weight, eps, cache, positions, q_out, k_out, v_out):
+        _ndim(4, q=q, k=k, v=v, q_out=q_out, k_out=k_out, v_out=v_out)
+        _ndim(1, q_weight=q_weight, k_weight=k_weight, positions=positions)
+        _ndim(2, cache=cache)
+        if cache.shape[1] != 96:
+            raise ValueError(f"the RoPE cache must be [N, 96], got {tuple(cache.shape)}")
+        device = _bf16(q, k, v, q_weight, k_weight, cache, q_out, k_out, v_out)
+        if positions.device != device or positions.dtype not in (torch.int32, torch.int64):
+            raise ValueError("positions must be an int32 or int64 tensor on the device of q")
+        if positions.dtype != torch.int64:
+            positions = positions.to(torch.int64)
+        _lib.launch("launch_h3_qkv_norm_rope_pack", device, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v),
+                    _lib.tensor(q_weight), _lib.tensor(k_weight), _lib.scalar(eps), _lib.tensor(cache[:, :48]),
+                    _lib.tensor(cache[:, 48:]), _lib.tensor(positions), _lib.tensor(q_out), _lib.tensor(k_out),
+                    _lib.tensor(v_out))
+
+    return kernel
 
 
 def make_qk_norm_rope_interleaved(dtype=None):

@@ -275,6 +275,16 @@ def qk_norm_rope(x, weight, eps, cos, sin, order="fixed", eps_rounding="bf16"):
     return rope_rotate_half(normalized, cos[:, None, None, :], sin[:, None, None, :])
 
 
+def qkv_norm_rope_pack(q, k, v, q_weight, k_weight, eps, cache, positions):
+    """One head group of InfiniLM's sequence-parallel attention input
+    (patches/InfiniLM.patch:1071-1110): the cache rows gathered by position
+    (:1077-1080), q and k through qk_norm_rope, v unchanged. q, k, v
+    [T, P, Hs, 128]; cache [N, 96]; positions [T]. Returns (q_out, k_out, v_out)."""
+    rows = cache[positions.long()]
+    cos, sin = rows[:, :48], rows[:, 48:]
+    return qk_norm_rope(q, q_weight, eps, cos, sin), qk_norm_rope(k, k_weight, eps, cos, sin), v.clone()
+
+
 def qk_norm_rope_interleaved(x, weight, eps, cos, sin, order="fixed", eps_rounding="bf16"):
     """Per-head RMSNorm (W = 128) then interleaved-pair RoPE, cos/sin [T, 64]."""
     normalized = rms_norm(x, weight, eps, order, eps_rounding)

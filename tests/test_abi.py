@@ -125,6 +125,15 @@ CASES = [
      + [t([4, 1, 2, 128])] * 3, "weight 64"),
     ("launch_h3_qk_norm_rope_interleaved", [t([4, 1, 2, 128]), t([128]), scal(), t([4, 48]), t([4, 48]),
                                             t([4, 1, 2, 128])], "interleaved needs a 64-wide table"),
+    ("launch_h3_qkv_norm_rope_pack", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([9, 48]),
+                                      t([9, 48]), t([5])] + [t([4, 2, 3, 128])] * 3, "positions length"),
+    ("launch_h3_qkv_norm_rope_pack", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([9, 64]),
+                                      t([9, 64]), t([4])] + [t([4, 2, 3, 128])] * 3, "table width 64"),
+    ("launch_h3_qkv_norm_rope_pack", [t([4, 2, 3, 128]), t([4, 2, 3, 128]), t([4, 3, 2, 128]), t([128]),
+                                      t([128]), scal(), t([9, 48]), t([9, 48]), t([4])]
+     + [t([4, 2, 3, 128])] * 3, "v shape"),
+    ("launch_h3_qkv_norm_rope_pack", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([0, 48]),
+                                      t([0, 48]), t([4])] + [t([4, 2, 3, 128])] * 3, "empty cache"),
     ("launch_h3_rope_cache", [t([4, 3]), t([15]), t([4, 48]), t([4, 48])], "15 powers"),
     ("launch_h3_rope_cache", [t([4, 2]), t([16]), t([4, 48]), t([4, 48])], "2 position axes"),
     ("launch_h3_full_attention", [t([1, 2, 8, 64]), t([1, 2, 8, 64]), t([1, 2, 8, 64]), scal(0.1),
@@ -168,6 +177,8 @@ EMPTY = [
     ("launch_h3_qk_norm_rope", [t([0, 1, 2, 128])] * 3 + [t([128])] * 3 + [scal(), t([0, 48]), t([0, 48])]
      + [t([0, 1, 2, 128])] * 3),
     ("launch_h3_rope_cache", [t([0, 3]), t([16]), t([0, 48]), t([0, 48])]),
+    ("launch_h3_qkv_norm_rope_pack", [t([0, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([0, 48]),
+                                      t([0, 48]), t([0])] + [t([0, 2, 3, 128])] * 3),
     ("launch_h3_full_attention", [t([1, 2, 0, 128]), t([1, 2, 8, 128]), t([1, 2, 8, 128]), scal(0.1),
                                   t([1, 2, 0, 128])]),
 ]
