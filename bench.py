@@ -141,7 +141,16 @@ def bench_pointwise(pkg, device) -> dict:
     nbytes = 6 * T * H * 128 * 2 + T * 8 + T * 96 * 2 + 2 * 128 * 2
     ms = time_graph([lambda i=i, o=o: k_pack(*i, w, w, 1e-6, table48, positions, *o) for i, o in views])
     record("qkv_norm_rope_pack", ms, nbytes, [T, 1, H, 128])
-    del projs, sends, views
+    # The same with the fp8 epilogue: q and k leave as e4m3 codes.
+    codes = [torch.empty(2, 1, T, H, 128, dtype=torch.float8_e4m3fn, device=device) for _ in range(3)]
+    descales = torch.empty(2, H, device=device)
+    views8 = [(i, [c[0].permute(1, 0, 2, 3), c[1].permute(1, 0, 2, 3), o[2]]) for (i, o), c in zip(views, codes)]
+    k_pack8 = pkg.make_qkv_norm_rope_pack_fp8()
+    nbytes = 3 * T * H * 128 * 2 + 2 * T * H * 128 + T * H * 128 * 2 + T * 8 + T * 96 * 2 + 2 * 128 * 2
+    ms = time_graph([lambda i=i, o=o: k_pack8(*i, w, w, 1e-6, table48, positions, *o, descales[0], descales[1])
+                     for i, o in views8])
+    record("qkv_norm_rope_pack_fp8", ms, nbytes, [T, 1, H, 128])
+    del projs, sends, views, codes, views8
 
     S, C, F = 8192, 7168, 18432
     rot = 3

@@ -238,6 +238,27 @@ NineToothedResult launch_h3_qkv_norm_rope_pack(NineToothedStream stream, NineToo
                                                NineToothedTensor q_out, NineToothedTensor k_out,
                                                NineToothedTensor v_out);
 
+/* launch_h3_qkv_norm_rope_pack with an fp8 epilogue for q and k, the producer
+ * of launch_h3_full_attention_fp8's q8 / k8: q8, k8 are uint8 e4m3fn codes
+ * [T, P, Hs, 128] (any strides; 8-byte aligned rows for the vector path),
+ * codes = e4m3fn(sat(bf16(y) * 448 / bound)) where y is the value
+ * launch_h3_qkv_norm_rope_pack writes and bound = fp32(sqrt(128) * 1.03125) *
+ * max|weight|, an upper bound of |y| that RMSNorm + RoPE guarantee for any
+ * input, so no absmax pass over the data is needed; q_descale, k_descale:
+ * fp32 [P * Hs] (contiguous), every head receives bound / 448 (1 for a zero
+ * weight). v_out: bf16 as before (V's scale depends on its data: quantise it
+ * with launch_h3_quantize_fp8_per_head).
+ * No counterpart in the reference (it has no fp8 path); callers are the fp8
+ * attention users, at the same site as launch_h3_qkv_norm_rope_pack. */
+NineToothedResult launch_h3_qkv_norm_rope_pack_fp8(NineToothedStream stream, NineToothedTensor q,
+                                                   NineToothedTensor k, NineToothedTensor v,
+                                                   NineToothedTensor q_weight, NineToothedTensor k_weight,
+                                                   NineToothedTensor eps, NineToothedTensor cos,
+                                                   NineToothedTensor sin, NineToothedTensor positions,
+                                                   NineToothedTensor q8, NineToothedTensor k8,
+                                                   NineToothedTensor v_out, NineToothedTensor q_descale,
+                                                   NineToothedTensor k_descale);
+
 /* The same RMSNorm followed by an interleaved-pair RoPE over all 128
  * channels: pair i = channels (2i, 2i+1), angle table cos/sin [T, 64]
  * (rotary channels split 32/48/48 over the t/h/w axes). Per-step bf16

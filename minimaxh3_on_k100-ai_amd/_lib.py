@@ -36,6 +36,7 @@ ENTRY_POINTS = {
     "launch_h3_qk_norm_rope": 12,
     "launch_h3_qk_norm_rope_interleaved": 6,
     "launch_h3_qkv_norm_rope_pack": 12,
+    "launch_h3_qkv_norm_rope_pack_fp8": 14,
     "launch_h3_rope_cache": 4,
 }
 

@@ -111,6 +111,17 @@ __host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv 
     return static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> f.shift);
 }
 
+// True when a byte view has unit inner stride and every row start (and the
+// base) is 8-byte aligned, so each 8 consecutive bytes can go as one store.
+template <int N>
+inline bool rows_vec8_bytes(const View<N> &v) {
+    if (v.shape[N - 1] > 1 && v.stride[N - 1] != 1) return false;
+    if ((reinterpret_cast<uintptr_t>(v.data) & 7) != 0 || v.shape[N - 1] % 8 != 0) return false;
+    for (int i = 0; i < N - 1; ++i)
+        if (v.shape[i] > 1 && v.stride[i] % 8 != 0) return false;
+    return true;
+}
+
 inline hipStream_t as_stream(NineToothedStream s) { return static_cast<hipStream_t>(s); }
 
 // Launch epilogue shared by all launchers: the launch status of the kernel.

@@ -19,7 +19,7 @@ __all__ = [
     "make_gated_residual_rms_modulate", "make_rope", "make_qk_norm_rope",
     "make_qk_norm_rope_interleaved", "make_rope_cache", "modulation_columns", "make_rms_modulate_indexed",
     "make_gated_residual_rms_modulate_indexed", "make_gated_residual_indexed", "qkv_by_rank",
-    "make_qkv_norm_rope_pack",
+    "make_qkv_norm_rope_pack", "make_qkv_norm_rope_pack_fp8",
 ]
 
 
@@ -301,6 +301,45 @@ def make_qkv_norm_rope_pack(dtype=None):
                     _lib.tensor(q_weight), _lib.tensor(k_weight), _lib.scalar(eps), _lib.tensor(cache[:, :48]),
                     _lib.tensor(cache[:, 48:]), _lib.tensor(positions), _lib.tensor(q_out), _lib.tensor(k_out),
                     _lib.tensor(v_out))
+
+    return kernel
+
+
+def _positions(positions: torch.Tensor, device) -> torch.Tensor:
+    if positions.device != device or positions.dtype not in (torch.int32, torch.int64):
+        raise ValueError("positions must be an int32 or int64 tensor on the device of q")
+    return positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+
+
+def make_qkv_norm_rope_pack_fp8(dtype=None):
+    """make_qkv_norm_rope_pack with q and k written as e4m3fn codes for the fp8
+    attention: codes = e4m3fn(sat(bf16(y) * 448 / bound)), bound =
+    fp32(sqrt(128) * 1.03125) * max|weight| (an upper bound of |y| for any
+    input, so no absmax pass). Returns kernel(q, k, v, q_weight, k_weight, eps,
+    cache, positions, q8, k8, v_out, q_descale, k_descale): q8, k8
+    torch.float8_e4m3fn (or uint8) [T, P, Hs, 128]; q_descale, k_descale fp32
+    [P * Hs] receive bound / 448; v_out bf16 (quantise it with
+    quantize_fp8_per_head). No counterpart in the reference."""
+    _bf16_only(dtype)
+
+    def kernel(q, k, v, q_weight, k_weight, eps, cache, positions, q8, k8, v_out, q_descale, k_descale):
+        _ndim(4, q=q, k=k, v=v, q8=q8, k8=k8, v_out=v_out)
+        _ndim(1, q_weight=q_weight, k_weight=k_weight, positions=positions, q_descale=q_descale,
+              k_descale=k_descale)
+        _ndim(2, cache=cache)
+        if cache.shape[1] != 96:
+            raise ValueError(f"the RoPE cache must be [N, 96], got {tuple(cache.shape)}")
+        device = _bf16(q, k, v, q_weight, k_weight, cache, v_out)
+        _lib.check_cuda(q, q8, k8, q_descale, k_descale)
+        for name, t in (("q8", q8), ("k8", k8)):
+            if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
+                raise ValueError(f"{name} must be float8_e4m3fn or uint8, got {t.dtype}")
+        _lib.check_dtype(torch.float32, q_descale, k_descale)
+        positions = _positions(positions, device)
+        _lib.launch("launch_h3_qkv_norm_rope_pack_fp8", device, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v),
+                    _lib.tensor(q_weight), _lib.tensor(k_weight), _lib.scalar(eps), _lib.tensor(cache[:, :48]),
+                    _lib.tensor(cache[:, 48:]), _lib.tensor(positions), _lib.tensor(q8), _lib.tensor(k8),
+                    _lib.tensor(v_out), _lib.tensor(q_descale), _lib.tensor(k_descale))
 
     return kernel
 

@@ -285,6 +285,34 @@ def qkv_norm_rope_pack(q, k, v, q_weight, k_weight, eps, cache, positions):
     return qk_norm_rope(q, q_weight, eps, cos, sin), qk_norm_rope(k, k_weight, eps, cos, sin), v.clone()
 
 
+QK_FP8_BOUND_PER_WEIGHT = torch.tensor(math.sqrt(128) * 1.03125, dtype=F32)
+
+
+def qk_fp8_descale(weight: torch.Tensor) -> torch.Tensor:
+    """bound / 448 with bound = fp32(sqrt(128) * 1.03125) * max|weight| (fp32):
+    the scale of the q/k fp8 epilogue (1 for a zero weight). The bound holds
+    for every output of qk_norm_rope with this weight; tests/test_qkv_pack.py
+    checks it on adversarial inputs."""
+    bound = QK_FP8_BOUND_PER_WEIGHT * weight.float().abs().max()
+    return torch.where(bound > 0, bound / E4M3_MAX, torch.ones_like(bound)), bound
+
+
+def quantize_fp8_with_bound(y: torch.Tensor, bound: torch.Tensor) -> torch.Tensor:
+    """e4m3fn(sat(y * (448 / bound))) in fp32 (0 codes for bound 0)."""
+    inv = torch.where(bound > 0, E4M3_MAX / bound, torch.zeros_like(bound))
+    return (y.float() * inv).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+
+
+def qkv_norm_rope_pack_fp8(q, k, v, q_weight, k_weight, eps, cache, positions):
+    """qkv_norm_rope_pack with q and k quantised by the weight bound. Returns
+    (q8, k8, v, q_descale, k_descale); descales are per tensor (every head
+    shares the weight)."""
+    q_out, k_out, v_out = qkv_norm_rope_pack(q, k, v, q_weight, k_weight, eps, cache, positions)
+    qd, qb = qk_fp8_descale(q_weight)
+    kd, kb = qk_fp8_descale(k_weight)
+    return quantize_fp8_with_bound(q_out, qb), quantize_fp8_with_bound(k_out, kb), v_out, qd, kd
+
+
 def qk_norm_rope_interleaved(x, weight, eps, cos, sin, order="fixed", eps_rounding="bf16"):
     """Per-head RMSNorm (W = 128) then interleaved-pair RoPE, cos/sin [T, 64]."""
     normalized = rms_norm(x, weight, eps, order, eps_rounding)

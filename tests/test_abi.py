@@ -134,6 +134,12 @@ CASES = [
      + [t([4, 2, 3, 128])] * 3, "v shape"),
     ("launch_h3_qkv_norm_rope_pack", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([0, 48]),
                                       t([0, 48]), t([4])] + [t([4, 2, 3, 128])] * 3, "empty cache"),
+    ("launch_h3_qkv_norm_rope_pack_fp8", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([9, 48]),
+                                          t([9, 48]), t([4])] + [t([4, 2, 3, 128])] * 3 + [t([5]), t([6])],
+     "descale length"),
+    ("launch_h3_qkv_norm_rope_pack_fp8", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([9, 48]),
+                                          t([9, 48]), t([4]), t([4, 2, 3, 64]), t([4, 2, 3, 128]),
+                                          t([4, 2, 3, 128]), t([6]), t([6])], "q8 width"),
     ("launch_h3_rope_cache", [t([4, 3]), t([15]), t([4, 48]), t([4, 48])], "15 powers"),
     ("launch_h3_rope_cache", [t([4, 2]), t([16]), t([4, 48]), t([4, 48])], "2 position axes"),
     ("launch_h3_full_attention", [t([1, 2, 8, 64]), t([1, 2, 8, 64]), t([1, 2, 8, 64]), scal(0.1),

@@ -12,6 +12,11 @@ both launch shapes, a generic-stride layout and clamped positions.
 """
 from __future__ import annotations
 
+import math
+import re
+from pathlib import Path
+
+import numpy as np
 import pytest
 import torch
 
@@ -118,3 +123,113 @@ def test_qkv_pack_generic_strides_and_clamped_positions(pkg, oracle, device):
     torch.cuda.synchronize()
     for name, got, want in zip("qkv", outs, ref):
         assert_bitwise(got, want, f"strided {name}")
+
+
+# ------------------------------------------------------------------ fp8 epilogue
+
+
+def test_qk_fp8_bound_holds_on_adversarial_inputs(oracle):
+    """|qk_norm_rope(x)| <= fp32(sqrt(128) * 1.03125) * max|w| for inputs that
+    put all of a head's energy in one channel or one rotated pair, at angles
+    that keep it there, and for random heads; and the bound is tight within
+    10% (a one-hot pass-through channel reaches sqrt(128) * w)."""
+    gen = torch.Generator().manual_seed(11)
+    rows = []
+    for i in range(128):  # one-hot heads, each sign
+        for sign in (1.0, -1.0):
+            x = torch.zeros(128)
+            x[i] = sign * 3.0
+            rows.append(x)
+    for i in range(48):  # energy split over a rotate-half pair
+        x = torch.zeros(128)
+        x[i], x[i + 48] = 2.0, -2.0
+        rows.append(x)
+    rows += list(torch.randn(64, 128, generator=gen) * 4)
+    x = torch.stack(rows).to(BF).view(-1, 1, 1, 128)
+    T = x.shape[0]
+    for w in ((torch.rand(128, generator=gen) * 0.5 + 0.75).to(BF), torch.ones(128, dtype=BF),
+              (torch.randn(128, generator=gen) * 2).to(BF)):
+        for theta in (0.0, math.pi / 4, math.pi / 2, 1.0, 2.5):
+            cos = torch.full((T, 48), math.cos(theta)).to(BF)
+            sin = torch.full((T, 48), math.sin(theta)).to(BF)
+            y = oracle.qk_norm_rope(x, w, 1e-6, cos, sin).float()
+            _, bound = oracle.qk_fp8_descale(w)
+            assert float(y.abs().max()) <= float(bound), (theta, float(y.abs().max()), float(bound))
+        # Tightness: one-hot at the largest-|w| pass-through channel, angle 0.
+        j = 96 + int(w[96:].float().abs().argmax())
+        xh = torch.zeros(1, 1, 1, 128)
+        xh[..., j] = 1.0
+        y = oracle.qk_norm_rope(xh.to(BF), w, 1e-6, cos[:1] * 0 + 1, sin[:1] * 0).float()
+        assert float(y.abs().max()) >= 0.9 * math.sqrt(128) * float(w[96:].float().abs().max())
+
+
+def test_kernel_bound_constant_is_the_oracles():
+    text = (Path(__file__).resolve().parents[1] / "minimaxh3_on_k100-ai_amd" / "csrc" / "h3_pointwise.hip").read_text()
+    literal = re.search(r"kQkFp8BoundPerWeight = ([0-9.]+)f", text).group(1)
+    assert np.float32(float(literal)) == np.float32(math.sqrt(128) * 1.03125)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,P,Hs", [(1024, 2, 7), (8192, 1, 14), (77, 4, 3)], ids=["1024x2x7", "8192x1x14", "77x4x3"])
+def test_qkv_pack_fp8_codes(pkg, oracle, device, T, P, Hs):
+    projected, wq, wk, cache, positions = _case(T, P, Hs, 3 * T + P, device)
+    wk = (wk.float() * 1.7).to(BF)  # a different bound for k
+    q, k, v = pkg.qkv_by_rank(projected, P)
+    q8_ref, k8_ref, v_ref, qd_ref, kd_ref = oracle.qkv_norm_rope_pack_fp8(q, k, v, wq, wk, 1e-6, cache, positions)
+    qd, kd, vd = pkg.qkv_by_rank(projected.to(device), P)
+    codes = [torch.zeros(P, T, Hs, 128, dtype=torch.float8_e4m3fn, device=device) for _ in range(2)]
+    q8, k8 = (c.permute(1, 0, 2, 3) for c in codes)
+    v_out = torch.full((T, P, Hs, 128), float("nan"), dtype=BF, device=device)
+    q_descale = torch.zeros(P * Hs, device=device)
+    k_descale = torch.zeros(P * Hs, device=device)
+    pkg.make_qkv_norm_rope_pack_fp8()(qd, kd, vd, wq.to(device), wk.to(device), 1e-6, cache.to(device),
+                                      positions.to(device), q8, k8, v_out, q_descale, k_descale)
+    torch.cuda.synchronize()
+    assert torch.equal(q8.cpu().view(torch.uint8), q8_ref.view(torch.uint8))
+    assert torch.equal(k8.cpu().view(torch.uint8), k8_ref.view(torch.uint8))
+    assert_bitwise(v_out, v_ref, "v")
+    assert torch.equal(q_descale.cpu(), qd_ref.expand(P * Hs))
+    assert torch.equal(k_descale.cpu(), kd_ref.expand(P * Hs))
+
+
+@pytest.mark.gpu
+def test_qkv_pack_fp8_feeds_fp8_attention(pkg, oracle, device):
+    """Producer q8 / k8 (weight-bound scales) and the quantiser's v8 into the
+    all-fp8 attention lose no accuracy against absmax-scaled q8 / k8 of the same
+    bf16 values through the same kernel (relative RMS against fp32 attention
+    within 2e-3 of it). The all-fp8 recipe itself sits at about 5.3e-2 on these
+    RMSNorm'd inputs (the CPU emulation gives the same figure for both
+    scalings), hence the 6e-2 ceiling; the fp8 P.V variant stays under 5e-2."""
+    T, H = 2048, 4
+    projected, wq, wk, cache, positions = _case(T, 1, H, 99, device)
+    qd, kd, vd = pkg.qkv_by_rank(projected.to(device), 1)
+    wqd, wkd, cd, pd = wq.to(device), wk.to(device), cache.to(device), positions.to(device)
+    q8 = torch.empty(1, H, T, 128, dtype=torch.float8_e4m3fn, device=device)
+    k8 = torch.empty_like(q8)
+    v_out = torch.empty(1, T, H, 128, dtype=BF, device=device)
+    q_descale, k_descale = torch.empty(H, device=device), torch.empty(H, device=device)
+    # [T, 1, H, 128] views of the [1, H, T, 128] attention layouts.
+    as_tph = lambda t: t[0].permute(1, 0, 2).unsqueeze(1)  # noqa: E731
+    pkg.make_qkv_norm_rope_pack_fp8()(qd, kd, vd, wqd, wkd, 1e-6, cd, pd, as_tph(q8), as_tph(k8),
+                                      v_out.view(T, 1, H, 128), q_descale, k_descale)
+    qb, kb = torch.empty(T, 1, H, 128, dtype=BF, device=device), torch.empty(T, 1, H, 128, dtype=BF, device=device)
+    pkg.make_qkv_norm_rope_pack()(qd, kd, vd, wqd, wkd, 1e-6, cd, pd, qb, kb, torch.empty_like(qb))
+    to_bhsd = lambda t: t.view(1, T, H, 128).transpose(1, 2)  # noqa: E731
+    v = to_bhsd(v_out)
+    v8, v_descale = pkg.quantize_fp8_per_head(v, transposed=True)
+    qa, qad = pkg.quantize_fp8_per_head(to_bhsd(qb))
+    ka, kad = pkg.quantize_fp8_per_head(to_bhsd(kb))
+    scale = 128 ** -0.5
+    out, out_amax, out_pv = (torch.empty(1, H, T, 128, dtype=BF, device=device) for _ in range(3))
+    pkg.make_attention_fp8()(q8, k8, v8, q_descale, k_descale, v_descale, scale, out)
+    pkg.make_attention_fp8()(qa, ka, v8, qad, kad, v_descale, scale, out_amax)
+    pkg.make_attention_fp8pv()(to_bhsd(qb), to_bhsd(kb), v8, v_descale, scale, out_pv)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_bhsd(qb).cpu(), to_bhsd(kb).cpu(), v.cpu(), scale, dtype=torch.float32).double()
+
+    def rel(o):
+        return float((o.cpu().double() - ref).norm() / ref.norm())
+
+    r_prod, r_amax, r_pv = rel(out), rel(out_amax), rel(out_pv)
+    assert r_prod <= r_amax + 2e-3, (r_prod, r_amax)
+    assert r_prod <= 6e-2 and r_pv <= 5e-2, (r_prod, r_pv)
