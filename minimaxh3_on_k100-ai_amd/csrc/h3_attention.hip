@@ -66,7 +66,12 @@ struct AttnArgs {
     int B, H, Sq, Sk;
     int qblocks;                          // ceil(Sq / kBM)
     float c;                              // scale * log2(e)
+    int k_bytes, v_bytes;                 // buffer-load path: byte extent of one head's K / V rows
 };
+
+// The dword-3 word of a raw buffer descriptor on gfx9 (CDNA): no format
+// conversion, bounds checked against num_records in bytes.
+constexpr int kBufferWord3 = 0x00020000;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -94,6 +99,17 @@ __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, 
         const int row = row0 < valid ? row0 : valid - 1;
         reg[r] = *reinterpret_cast<const u32x4_t *>(base + static_cast<int64_t>(key0 + row) * s_stride + (t % 16) * 8);
     }
+}
+
+// The same tile through buffer loads: per-thread byte offsets fixed for the
+// kernel (voff) plus the tile's uniform byte offset (soff). Rows past the
+// head's last key fall outside the descriptor's range and read as zero
+// (their scores are masked), so no address is clamped and no VALU is spent on
+// addresses per tile.
+__device__ __forceinline__ void load_tile_buf(__amdgpu_buffer_rsrc_t rs, const int (&voff)[kLoadRows], int soff,
+                                              u32x4_t (&reg)[kLoadRows]) {
+#pragma unroll
+    for (int r = 0; r < kLoadRows; ++r) reg[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[r], soff, 0);
 }
 
 template <int PITCH>
@@ -229,7 +245,9 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
     __builtin_amdgcn_sched_group_barrier(0x008, 2 * kQS, 0);
 }
 
-template <bool NEG>
+// BUF: K and V tiles through buffer loads (the host checks that one head's
+// rows fit a 31-bit byte range and that rows do not overlap).
+template <bool NEG, bool BUF>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElemsK];
     __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElemsV];
@@ -279,8 +297,27 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     }
 
     u32x4_t kreg[kLoadRows], vreg[kLoadRows];
-    load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
-    load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+    // Descriptors of this head's K and V rows (range 0 on the pointer path, never used there).
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(kbase), static_cast<short>(0), a.k_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(vbase), static_cast<short>(0), a.v_bytes, kBufferWord3);
+    int kvoff[kLoadRows], vvoff[kLoadRows];
+    const int kstep = static_cast<int>(a.ks[2]) * 2 * kBN, vstep = static_cast<int>(a.vs[2]) * 2 * kBN;
+    if constexpr (BUF) {
+#pragma unroll
+        for (int r = 0; r < kLoadRows; ++r) {
+            const int row = static_cast<int>(threadIdx.x) / 16 + (kThreadsWG / 16) * r;
+            const int chunk = static_cast<int>(threadIdx.x) % 16 * 8;
+            kvoff[r] = (row * static_cast<int>(a.ks[2]) + chunk) * 2;
+            vvoff[r] = (row * static_cast<int>(a.vs[2]) + chunk) * 2;
+        }
+        load_tile_buf(krs, kvoff, 0, kreg);
+        load_tile_buf(vrs, vvoff, 0, vreg);
+    } else {
+        load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
+        load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+    }
     store_tile<kRowK>(lds_k[0], kreg);
     store_tile<kRowV>(lds_v[0], vreg);
     __syncthreads();
@@ -299,7 +336,11 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         const int buf = tile & 1;
         const int next0 = (tile + 1) * kBN;
         const bool has_next = next0 < a.Sk;
-        {
+        if constexpr (BUF) {
+            // After the last tile the loads fall past the rows and read zeros (unused).
+            load_tile_buf(krs, kvoff, (tile + 1) * kstep, kreg);
+            load_tile_buf(vrs, vvoff, (tile + 1) * vstep, vreg);
+        } else {
             // After the last tile the loads re-read the last row (unused), so
             // they need no branch either.
             const int n0 = has_next ? next0 : a.Sk - 1;
@@ -381,9 +422,30 @@ extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, 
     const int64_t grid = static_cast<int64_t>(a.B) * a.H * a.qblocks;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     a.c = static_cast<float>(static_cast<float>(sc) * kLog2e);
-    if (a.c < 0.0f)
-        attention_fwd_kernel<true><<<static_cast<unsigned>(grid), kThreadsWG, 0, as_stream(stream)>>>(a);
-    else
-        attention_fwd_kernel<false><<<static_cast<unsigned>(grid), kThreadsWG, 0, as_stream(stream)>>>(a);
+    // Buffer loads when one head's K / V rows (plus one tile of key offsets
+    // past the end, which the last iteration's unused loads reach) fit a
+    // 31-bit byte range and rows do not overlap.
+    auto extent = [&](int64_t stride) -> int64_t {
+        return stride >= kD ? (static_cast<int64_t>(a.Sk) - 1) * stride * 2 + kD * 2 : -1;
+    };
+    const int64_t k_ext = extent(a.ks[2]), v_ext = extent(a.vs[2]);
+    const int64_t reach = (static_cast<int64_t>(a.Sk) + 2 * kBN) * 2 *
+                          (a.ks[2] > a.vs[2] ? a.ks[2] : a.vs[2]);
+    const bool buf = k_ext > 0 && v_ext > 0 && reach < (int64_t{1} << 31);
+    a.k_bytes = buf ? static_cast<int>(k_ext) : 0;
+    a.v_bytes = buf ? static_cast<int>(v_ext) : 0;
+    const unsigned g = static_cast<unsigned>(grid);
+    hipStream_t st = as_stream(stream);
+    if (a.c < 0.0f) {
+        if (buf)
+            attention_fwd_kernel<true, true><<<g, kThreadsWG, 0, st>>>(a);
+        else
+            attention_fwd_kernel<true, false><<<g, kThreadsWG, 0, st>>>(a);
+    } else {
+        if (buf)
+            attention_fwd_kernel<false, true><<<g, kThreadsWG, 0, st>>>(a);
+        else
+            attention_fwd_kernel<false, false><<<g, kThreadsWG, 0, st>>>(a);
+    }
     return launch_status();
 }

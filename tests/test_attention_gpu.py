@@ -78,6 +78,28 @@ def test_attention_packed_qkv(pkg, oracle, device):
     assert torch.equal(first, out)
 
 
+def test_attention_broadcast_keys_take_the_pointer_path(pkg, oracle, device):
+    """K and V broadcast along S (stride 0: every key the same row), which the
+    buffer-load path does not take (its rows must not overlap): softmax is
+    uniform, so every output row equals the V row; also Sk not a multiple of 64
+    and a second head with its own row."""
+    gen = torch.Generator("cpu").manual_seed(9)
+    Sq, Sk, H = 150, 333, 2
+    q = torch.randn(1, H, Sq, 128, generator=gen).to(BF)
+    krow = torch.randn(1, H, 1, 128, generator=gen).to(BF)
+    vrow = torch.randn(1, H, 1, 128, generator=gen).to(BF)
+    k, v = krow.expand(1, H, Sk, 128), vrow.expand(1, H, Sk, 128)
+    kd, vd = krow.to(device).expand(1, H, Sk, 128), vrow.to(device).expand(1, H, Sk, 128)
+    assert kd.stride(2) == 0 and vd.stride(2) == 0
+    out = torch.empty(1, H, Sq, 128, dtype=BF, device=device)
+    pkg.make_attention()(q.to(device), kd, vd, 128 ** -0.5, out)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q, k.contiguous(), v.contiguous(), 128 ** -0.5)
+    mx, rel = attention_error(out.cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+    assert (out.cpu().float() - vrow.float()).abs().max().item() <= 2 ** -7 * vrow.float().abs().max().item()
+
+
 def test_attention_scale_edge_cases(pkg, oracle, device):
     gen = torch.Generator("cpu").manual_seed(5)
     q = torch.randn(1, 2, 130, 128, generator=gen).to(BF)
