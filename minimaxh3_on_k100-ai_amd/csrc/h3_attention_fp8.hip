@@ -73,7 +73,12 @@ struct Fp8Args {
     int64_t qs[3], ks[3], vs0, vs1, vs3, os[3];
     int B, H, Sq, Sk, qblocks;
     float c;  // scale * log2(e)
+    int k_bytes, v_bytes;  // buffer-load path: byte extent of one head's K rows / V^T rows
 };
+
+// The dword-3 word of a raw buffer descriptor on gfx9 (CDNA): no format
+// conversion, bounds checked against num_records in bytes.
+constexpr int kBufferWord3 = 0x00020000;
 
 // ------------------------------------------------------------------ tiles
 
@@ -163,7 +168,10 @@ __device__ __forceinline__ void store_v(uint8_t *lds, const u32x4_t &reg) {
 
 // ------------------------------------------------------------------ kernel
 
-template <bool QK_FP8, bool NEG>
+// BUF: the main loop's full K and V^T tiles through buffer loads, each
+// thread's byte offsets fixed for the kernel and the tile's offset uniform (the
+// host checks that one head's rows fit a 31-bit byte range).
+template <bool QK_FP8, bool NEG, bool BUF>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fp8_kernel(
     Fp8Args a) {
     constexpr int kKBytes = kBN * (QK_FP8 ? 128 : 256);
@@ -359,12 +367,37 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
     using Partial = std::integral_constant<bool, true>;
     const int full = a.Sk / kBN;  // tiles 0 .. full-1 hold 64 keys
     int tile = 0;
+    // Buffer descriptors of this head's K rows and V^T rows (range 0 when unused).
+    constexpr int kKChunks = QK_FP8 ? 8 : 16;
+    constexpr int kKPerThread = kBN * kKChunks / kThreadsWG;
+    const int64_t k_row_bytes = a.ks[2] * (QK_FP8 ? 1 : 2);
+    const uint8_t *khead = QK_FP8 ? a.k8 + b * a.ks[0] + h * a.ks[1]
+                                  : reinterpret_cast<const uint8_t *>(a.k + b * a.ks[0] + h * a.ks[1]);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(khead),
+                                                                         static_cast<short>(0), a.k_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.v8 + b * a.vs0 + h * a.vs1), static_cast<short>(0), a.v_bytes, kBufferWord3);
+    int kvoff[kKPerThread], vvoff;
+#pragma unroll
+    for (int i = 0; i < kKPerThread; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * kThreadsWG;
+        kvoff[i] = (idx / kKChunks) * static_cast<int>(k_row_bytes) + 16 * (idx % kKChunks);
+    }
+    vvoff = (static_cast<int>(threadIdx.x) / 4) * static_cast<int>(a.vs3) + 16 * (static_cast<int>(threadIdx.x) % 4);
     // Main loop: the next tile is full, so its loads need no masks or branches.
     for (; tile + 1 < full; ++tile) {
         const int buf = tile & 1;
         u32x4_t kr[2], vr;
-        load_k_full<QK_FP8>(a, b, h, (tile + 1) * kBN, kr);
-        load_v_full(a, b, h, (tile + 1) * kBN, vr);
+        if constexpr (BUF) {
+            const int key1 = (tile + 1) * kBN;
+#pragma unroll
+            for (int i = 0; i < kKPerThread; ++i)
+                kr[i] = __builtin_amdgcn_raw_buffer_load_b128(krs, kvoff[i], key1 * static_cast<int>(k_row_bytes), 0);
+            vr = __builtin_amdgcn_raw_buffer_load_b128(vrs, vvoff, key1, 0);
+        } else {
+            load_k_full<QK_FP8>(a, b, h, (tile + 1) * kBN, kr);
+            load_v_full(a, b, h, (tile + 1) * kBN, vr);
+        }
         attend(Full{}, buf, kBN);
         store_k<QK_FP8>(lds_k[buf ^ 1], kr);
         store_v(lds_v[buf ^ 1], vr);
@@ -522,10 +555,26 @@ int launch_fp8(hipStream_t stream, const Fp8Args &a0) {
     a.qblocks = (a.Sq + kBM - 1) / kBM;
     const int64_t grid = static_cast<int64_t>(a.B) * a.H * a.qblocks;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
-    if (a.c < 0.0f)
-        attention_fp8_kernel<QK_FP8, true><<<static_cast<unsigned>(grid), kThreadsWG, 0, stream>>>(a);
-    else
-        attention_fp8_kernel<QK_FP8, false><<<static_cast<unsigned>(grid), kThreadsWG, 0, stream>>>(a);
+    // Buffer loads when one head's K rows (non-overlapping) and V^T rows (each
+    // at least Sk bytes apart) fit a 31-bit byte range.
+    const int64_t esize = QK_FP8 ? 1 : 2, k_row = a.ks[2] * esize;
+    const int64_t k_ext = k_row >= kD * esize ? (static_cast<int64_t>(a.Sk) - 1) * k_row + kD * esize : -1;
+    const int64_t v_ext = a.vs3 >= a.Sk ? (kD - 1) * a.vs3 + a.Sk : -1;
+    const bool buf = k_ext > 0 && v_ext > 0 && k_ext < (int64_t{1} << 31) && v_ext < (int64_t{1} << 31);
+    a.k_bytes = buf ? static_cast<int>(k_ext) : 0;
+    a.v_bytes = buf ? static_cast<int>(v_ext) : 0;
+    const unsigned g = static_cast<unsigned>(grid);
+    if (a.c < 0.0f) {
+        if (buf)
+            attention_fp8_kernel<QK_FP8, true, true><<<g, kThreadsWG, 0, stream>>>(a);
+        else
+            attention_fp8_kernel<QK_FP8, true, false><<<g, kThreadsWG, 0, stream>>>(a);
+    } else {
+        if (buf)
+            attention_fp8_kernel<QK_FP8, false, true><<<g, kThreadsWG, 0, stream>>>(a);
+        else
+            attention_fp8_kernel<QK_FP8, false, false><<<g, kThreadsWG, 0, stream>>>(a);
+    }
     return launch_status();
 }
 
