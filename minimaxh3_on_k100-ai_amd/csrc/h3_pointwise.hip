@@ -1178,9 +1178,34 @@ __device__ __forceinline__ RopeTab load_tab(const RopeArgs &a, uint32_t t, int l
     return tab;
 }
 
+// The reciprocal of a head row, bf16(1 / sqrt(var)) with IEEE sqrt and
+// division, for a var that is itself a bf16 value: with var = 1.m x 2^(2k + p),
+// sqrt and 1/x commute exactly with the power-of-two scaling (normal range), so
+// the result is T[p][m] x 2^-k where T holds the 256 values for p = 0, 1 and the
+// 7-bit mantissa m. The block builds T in LDS with the IEEE sequence itself;
+// zero, subnormal, infinite and NaN var take that sequence directly.
+constexpr int kRsqrtTable = 256;
+
+__device__ __forceinline__ void build_rsqrt_table(bf16_t *tab) {
+    for (int i = threadIdx.x; i < kRsqrtTable; i += blockDim.x) {
+        const float var = __uint_as_float((static_cast<uint32_t>(127 + (i >> 7)) << 23) | (static_cast<uint32_t>(i & 127) << 16));
+        tab[i] = static_cast<bf16_t>(__float_as_uint(rbf(rsqrt_ieee(var))) >> 16);
+    }
+}
+
+__device__ __forceinline__ float rsqrt_bf16(float var, const bf16_t *tab) {
+    const uint32_t b = __float_as_uint(var);
+    const int e = static_cast<int>((b >> 23) & 255u);
+    if (e == 0 || e == 255) return rbf(rsqrt_ieee(var));
+    const int ee = e - 127, p = ee & 1;
+    return __builtin_ldexpf(bf2f(tab[(p << 7) | ((b >> 16) & 127u)]), -((ee - p) >> 1));
+}
+
 // RMSNorm over the 128 channels held by a 16-lane row group (the same fixed
 // order as the rms family at W = 128), then weight: returns bf16 values in f.
-__device__ __forceinline__ void head_rms(float f[8], const float w[8], float eps_bf) {
+// `tab`: the block's reciprocal table (build_rsqrt_table), or null for the IEEE
+// sequence in every lane.
+__device__ __forceinline__ void head_rms(float f[8], const float w[8], float eps_bf, const bf16_t *tab = nullptr) {
     float partial = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -1189,7 +1214,13 @@ __device__ __forceinline__ void head_rms(float f[8], const float w[8], float eps
         partial += q0;
         partial += q1;
     }
-    const float r = rms_reciprocal(fold_lanes<16>(partial), 128, eps_bf);
+    float r;
+    if (tab != nullptr) {
+        const float mean = rbf(fold_lanes<16>(partial) * 0.0078125f);  // bf16(sum / 128): exact scaling
+        r = rsqrt_bf16(rbf(mean + eps_bf), tab);
+    } else {
+        r = rms_reciprocal(fold_lanes<16>(partial), 128, eps_bf);
+    }
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
         float n0 = f[e] * r, n1 = f[e + 1] * r;
@@ -1271,11 +1302,16 @@ __global__ __launch_bounds__(kThreads) void head_rows_kernel(RopeArgs a) {
     }
     float w[8];
     if constexpr (MODE != kRopeOnly) u4_to_f8(load_group<VEC>(a.w, a.w_stride, lane * 8, 128), w);
+    __shared__ bf16_t rs_tab[kRsqrtTable];
+    if constexpr (MODE != kRopeOnly) {
+        build_rsqrt_table(rs_tab);  // while the rows are in flight
+        __syncthreads();
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float f[8];
         u4_to_f8(xv[r], f);
-        if constexpr (MODE != kRopeOnly) head_rms(f, w, a.eps_bf);
+        if constexpr (MODE != kRopeOnly) head_rms(f, w, a.eps_bf, rs_tab);
         if constexpr (MODE == kNormRopeInterleaved) {
             rope_interleaved(f, tab[r]);
         } else {
@@ -1315,12 +1351,13 @@ __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
     };
     float w[8];
     if constexpr (MODE != kRopeOnly) u4_to_f8(load_group<VEC>(a.w, a.w_stride, lane * 8, 128), w);
+    __shared__ bf16_t rs_tab[kRsqrtTable];
     auto finish = [&](Batch &bt) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float f[8];
             u4_to_f8(bt.xv[r], f);
-            if constexpr (MODE != kRopeOnly) head_rms(f, w, a.eps_bf);
+            if constexpr (MODE != kRopeOnly) head_rms(f, w, a.eps_bf, rs_tab);
             if constexpr (MODE == kNormRopeInterleaved) {
                 rope_interleaved(f, bt.tab[r]);
             } else {
@@ -1332,6 +1369,10 @@ __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
     Batch A, B;
     uint32_t base = blockIdx.x * kGroups * R;
     load(base, A);
+    if constexpr (MODE != kRopeOnly) {
+        build_rsqrt_table(rs_tab);  // while the first batch is in flight
+        __syncthreads();
+    }
     while (true) {
         load(base + stride, B);
         finish(A);
@@ -1509,6 +1550,7 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
     };
     float w[8];
     u4_to_f8(load_group<VEC>(kind == 0 ? a.wq : a.wk, kind == 0 ? a.wq_stride : a.wk_stride, lane * 8, 128), w);
+    __shared__ bf16_t rs_tab[kRsqrtTable];
     float inv = 0.0f;
     if constexpr (FP8) {
         float mw = 0.0f;
@@ -1537,7 +1579,7 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
         for (int r = 0; r < R; ++r) {
             float f[8];
             u4_to_f8(bt.xv[r], f);
-            head_rms(f, w, a.eps_bf);
+            head_rms(f, w, a.eps_bf, rs_tab);
             rope_rotate_half(f, lane, bt.tab[r]);
             if constexpr (FP8) {
 #pragma unroll
@@ -1563,6 +1605,10 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
     Batch A, B;
     uint32_t tile = tile0;
     load(tile, A);
+    if (kind < 2) {  // uniform over the block: q and k blocks normalise
+        build_rsqrt_table(rs_tab);  // while the first batch is in flight
+        __syncthreads();
+    }
     while (true) {
         load(tile + tiles, B);
         finish(A);

@@ -249,6 +249,39 @@ def test_qk_norm_rope_matches_rms_then_rope(pkg, device):
     assert_bitwise(fused.view(T, H, 128), rotated, "fused vs unfused")
 
 
+@pytest.mark.parametrize("eps", [1e-6, 0.0])
+def test_head_rows_across_magnitudes(pkg, oracle, device, eps):
+    """Head rows scaled by 2^-70 .. 2^60 (var over every exponent parity,
+    subnormal var at the small end, infinite squares at the large end) and zero
+    rows (var = eps; 0 with eps = 0, so 0 * inf = NaN as in the reference), for
+    the three head-row kernels: rotate-half, interleaved and the q/k/v pack."""
+    gen = _gen(21)
+    T, H = 139, 4
+    x = torch.randn(T, 1, H, 128, generator=gen)
+    scales = 2.0 ** torch.arange(-70, 61, dtype=torch.float32)
+    x = x * scales[torch.arange(T * H) % scales.numel()].view(T, 1, H, 1)
+    x[::17, :, 1] = 0.0
+    x = x.to(BF)
+    w = _randn(gen, 128)
+    table48, table64 = _randn(gen, T, 96), _randn(gen, T, 128)
+    xd, wd = x.to(device), w.to(device)
+    out = torch.empty_like(xd)
+    pkg.make_qk_norm_rope()(xd, wd, eps, table48[:, :48].to(device), table48[:, 48:].to(device), out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.qk_norm_rope(x, w, eps, table48[:, :48], table48[:, 48:]), "rotate-half")
+    out = torch.empty_like(xd)
+    pkg.make_qk_norm_rope_interleaved()(xd, wd, eps, table64[:, :64].to(device), table64[:, 64:].to(device), out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.qk_norm_rope_interleaved(x, w, eps, table64[:, :64], table64[:, 64:]), "interleaved")
+    outs = [torch.empty_like(xd) for _ in range(3)]
+    positions = torch.arange(T)
+    pkg.make_qkv_norm_rope_pack()(xd, xd, xd, wd, wd, eps, table48.to(device), positions.to(device), *outs)
+    torch.cuda.synchronize()
+    q_ref, _, _ = oracle.qkv_norm_rope_pack(x, x, x, w, w, eps, table48, positions)
+    assert_bitwise(outs[0], q_ref, "q/k/v pack")
+    assert_bitwise(outs[1], q_ref, "q/k/v pack (k)")
+
+
 def test_qk_norm_rope_interleaved(pkg, oracle, device):
     q, k, w_q, w_k, pos = oracle.qk_norm_rope_inputs(T=2048, H=14, seed=3)
     cos, sin = oracle.rope_table_interleaved(pos)
