@@ -54,6 +54,17 @@ NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothed
                                            NineToothedTensor k, NineToothedTensor v,
                                            NineToothedTensor scale, NineToothedTensor o);
 
+/* The `bf16_prescale` numerics of the same operator: q enters the product as
+ * bf16(fp32(scale * log2(e)) * q) and the logits are used as they come
+ * (tools/h3_attention.py:87-101, selected by make_attention(numerics=
+ * "bf16_prescale"), :114). Same arguments and layouts as
+ * launch_h3_full_attention. The reference's AOT build names this launcher
+ * after its kernel_name (patches/ninetoothed.patch:138-146); this is the name
+ * the library exports for it. */
+NineToothedResult launch_h3_full_attention_bf16_prescale(NineToothedStream stream, NineToothedTensor q,
+                                                         NineToothedTensor k, NineToothedTensor v,
+                                                         NineToothedTensor scale, NineToothedTensor o);
+
 /* Per-head fp8 (OCP e4m3fn) quantisation for the fp8 attention variants.
  * x: bf16 [B, H, S, 128] (any strides on B/H/S, unit stride on D, 16-byte
  * aligned rows); x8: uint8 storage of e4m3fn codes, same shape, either

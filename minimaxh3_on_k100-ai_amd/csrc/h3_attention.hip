@@ -67,6 +67,7 @@ struct AttnArgs {
     int qblocks;                          // ceil(Sq / kBM)
     float c;                              // scale * log2(e)
     int k_bytes, v_bytes;                 // buffer-load path: byte extent of one head's K / V rows
+    bool prescale;                        // q enters the product as bf16(c q) and the logits are not rescaled
 };
 
 // The dword-3 word of a raw buffer descriptor on gfx9 (CDNA): no format
@@ -279,6 +280,17 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2] + 8 * half;
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) qreg[qs][kk] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 16 * kk));
+        if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const uint4 u = __builtin_bit_cast(uint4, qreg[qs][kk]);
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = pack2(lo2f(w[e]) * a.c, hi2f(w[e]) * a.c);
+                qreg[qs][kk] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
+            }
+        }
     }
 
     f32x16_t acc[4][kQS];  // O^T: dim block db (32 dims) x query block qs
@@ -330,6 +342,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     const int v_row_off = 8 * (g16 >> 1) + (s16 >> 2);
     const int v_col_off = 16 * (g16 & 1) + 4 * (s16 & 3);
 
+    // The logits' factor: c, or 1 when c is already in bf16(c q).
+    const float c_loop = a.prescale ? 1.0f : a.c;
     // Full tiles in the loop; a partial last tile (Sk % 64 != 0) after it.
     const int full = a.Sk / kBN;
     for (int tile = 0; tile < full; ++tile) {
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
             load_tile(kbase, a.ks[2], n0, nvalid, kreg);
             load_tile(vbase, a.vs[2], n0, nvalid, vreg);
         }
-        attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, a.c, krow, half, v_row_off,
+        attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, c_loop, krow, half, v_row_off,
                                 v_col_off);
         if (has_next) {
             store_tile<kRowK>(lds_k[buf ^ 1], kreg);
@@ -358,7 +372,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     }
     if (full * kBN < a.Sk) {
         const int buf = full & 1;
-        attend_tile<true, NEG>(lds_k[buf], lds_v[buf], a.Sk - full * kBN, qreg, acc, m_run, l_run, a.c, krow, half,
+        attend_tile<true, NEG>(lds_k[buf], lds_v[buf], a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, krow, half,
                                v_row_off, v_col_off);
     }
 
@@ -387,9 +401,12 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
 
 using namespace h3;
 
-extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothedTensor q,
-                                                      NineToothedTensor k, NineToothedTensor v,
-                                                      NineToothedTensor scale, NineToothedTensor o) {
+namespace {
+
+// The launcher of both numerics: fp32_qk (logits scaled by c = scale log2 e in
+// fp32) and bf16_prescale (q rounded to bf16(c q) before the product).
+int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedTensor k, NineToothedTensor v,
+                     NineToothedTensor scale, NineToothedTensor o, bool prescale) {
     View<4> qv, kv, vv, ov;
     double sc;
     if (!load_view(q, 2, qv) || !load_view(k, 2, kv) || !load_view(v, 2, vv) || !load_view(o, 2, ov) ||
@@ -422,6 +439,7 @@ extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, 
     const int64_t grid = static_cast<int64_t>(a.B) * a.H * a.qblocks;
     if (grid > static_cast<int64_t>(std::numeric_limits<int32_t>::max())) return kInvalid;
     a.c = static_cast<float>(static_cast<float>(sc) * kLog2e);
+    a.prescale = prescale;
     // Buffer loads when one head's K / V rows (plus one tile of key offsets
     // past the end, which the last iteration's unused loads reach) fit a
     // 31-bit byte range and rows do not overlap.
@@ -436,7 +454,7 @@ extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, 
     a.v_bytes = buf ? static_cast<int>(v_ext) : 0;
     const unsigned g = static_cast<unsigned>(grid);
     hipStream_t st = as_stream(stream);
-    if (a.c < 0.0f) {
+    if (a.c < 0.0f && !prescale) {  // the loop's max runs over c * s
         if (buf)
             attention_fwd_kernel<true, true><<<g, kThreadsWG, 0, st>>>(a);
         else
@@ -448,4 +466,18 @@ extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, 
             attention_fwd_kernel<false, false><<<g, kThreadsWG, 0, st>>>(a);
     }
     return launch_status();
+}
+
+}  // namespace
+
+extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothedTensor q,
+                                                      NineToothedTensor k, NineToothedTensor v,
+                                                      NineToothedTensor scale, NineToothedTensor o) {
+    return launch_attention(stream, q, k, v, scale, o, false);
+}
+
+extern "C" NineToothedResult launch_h3_full_attention_bf16_prescale(NineToothedStream stream, NineToothedTensor q,
+                                                                    NineToothedTensor k, NineToothedTensor v,
+                                                                    NineToothedTensor scale, NineToothedTensor o) {
+    return launch_attention(stream, q, k, v, scale, o, true);
 }

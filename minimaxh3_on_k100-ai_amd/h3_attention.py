@@ -12,6 +12,8 @@ Numerics (tools/h3_attention.py:25-101):
     scaled by scale*log2(e), exp2 online softmax, bf16 P for P.V, fp32
     denominator. On MFMA the P.V product always accumulates in place and only
     the last key tile is masked, so the three coincide.
+  - "bf16_prescale" (:87-101): q enters the product as bf16(fp32(scale log2 e) q)
+    and the logits are used unscaled (launch_h3_full_attention_bf16_prescale).
 Only head_dim 128 (the DiT's) is built; D = 72 (Qwen vision) is not.
 
 fp8 (no counterpart in the reference): `quantize_fp8_per_head` (per-head
@@ -26,7 +28,7 @@ from . import _lib
 
 __all__ = ["make_attention", "make_attention_fp8", "make_attention_fp8pv", "quantize_fp8_per_head", "NUMERICS"]
 
-NUMERICS = ("fp32_qk", "fp32_qk_dotacc", "fp32_qk_split")
+NUMERICS = ("fp32_qk", "fp32_qk_dotacc", "fp32_qk_split", "bf16_prescale")
 
 
 def _check_qkvo(q, k, v, out):
@@ -51,12 +53,14 @@ def make_attention(block_m=128, block_n=32, num_warps=4, num_stages=1, caller="t
     if dtype is not None and str(getattr(dtype, "name", dtype)).lower() not in ("bfloat16", "torch.bfloat16", "bf16"):
         raise ValueError(f"only the bfloat16 attention kernel is built, got dtype={dtype!r}")
 
+    entry = "launch_h3_full_attention_bf16_prescale" if numerics == "bf16_prescale" else "launch_h3_full_attention"
+
     def kernel(q, k, v, scale, out):
         _check_qkvo(q, k, v, out)
         device = _lib.check_cuda(q, k, v, out)
         _lib.check_dtype(torch.bfloat16, q, k, v, out)
-        _lib.launch("launch_h3_full_attention", device, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v),
-                    _lib.scalar(scale), _lib.tensor(out))
+        _lib.launch(entry, device, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.scalar(scale),
+                    _lib.tensor(out))
 
     return kernel
 

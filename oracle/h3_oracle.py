@@ -368,6 +368,15 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, d
     return out
 
 
+def attention_bf16_prescale(q, k, v, scale: float, dtype=torch.float64) -> torch.Tensor:
+    """The `bf16_prescale` numerics (tools/h3_attention.py:87-101): q rounded to
+    bf16(fp32(fp32(scale) * log2 e) * q) enters the product, whose value is a
+    base-2 logit; in natural units that is softmax(q' k^T ln 2) v."""
+    c = torch.tensor(scale, dtype=F32) * torch.tensor(1.4426950408889634, dtype=F32)
+    q_pre = (q.float() * c).to(BF16)
+    return attention(q_pre, k, v, math.log(2.0), dtype)
+
+
 def attention_rows(q, k, v, scale, rows: torch.Tensor, dtype=torch.float64) -> torch.Tensor:
     """The attention of selected query rows (the sampled-row check of
     tools/verify_attention.py:62-65)."""

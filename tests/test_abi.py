@@ -210,7 +210,7 @@ def test_python_factories_validate(pkg):
         pkg.make_qk_norm_rope(block_tokens=2, ranks=2)
     with pytest.raises(ValueError):
         pkg.make_swiglu(dtype="float16")
-    for numerics in ("fp32_qk", "fp32_qk_dotacc", "fp32_qk_split"):
+    for numerics in ("fp32_qk", "fp32_qk_dotacc", "fp32_qk_split", "bf16_prescale"):
         assert callable(pkg.make_attention(numerics=numerics))
 
 

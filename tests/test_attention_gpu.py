@@ -100,6 +100,21 @@ def test_attention_broadcast_keys_take_the_pointer_path(pkg, oracle, device):
     assert (out.cpu().float() - vrow.float()).abs().max().item() <= 2 ** -7 * vrow.float().abs().max().item()
 
 
+@pytest.mark.parametrize("scale", [128 ** -0.5, -0.07])
+def test_attention_bf16_prescale(pkg, oracle, device, scale):
+    """numerics="bf16_prescale" (tools/h3_attention.py:87-101) against its own
+    fp64 oracle, ragged Sq / Sk, positive and negative scale."""
+    gen = torch.Generator("cpu").manual_seed(17)
+    q = torch.randn(2, 3, 197, 128, generator=gen).to(BF)
+    k = torch.randn(2, 3, 333, 128, generator=gen).to(BF)
+    v = torch.randn(2, 3, 333, 128, generator=gen).to(BF)
+    out = torch.empty_like(q, device=device)
+    pkg.make_attention(numerics="bf16_prescale")(q.to(device), k.to(device), v.to(device), scale, out)
+    torch.cuda.synchronize()
+    mx, rel = attention_error(out.cpu(), oracle.attention_bf16_prescale(q, k, v, scale))
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
 def test_attention_scale_edge_cases(pkg, oracle, device):
     gen = torch.Generator("cpu").manual_seed(5)
     q = torch.randn(1, 2, 130, 128, generator=gen).to(BF)

@@ -451,3 +451,21 @@ def test_fp8_emulated_attention_error_budget():
     # With 1% of key rows x8 the e4m3 logits err by ~5% of up to ~30 log2
     # units: the all-fp8 recipe misses 5e-2, bf16 logits + fp8 P.V meet it.
     assert mixed <= 5e-2 and full > mixed, (full, mixed)
+
+
+def test_attention_bf16_prescale():
+    """bf16_prescale (tools/h3_attention.py:87-101): with a scale whose fp32
+    c = scale * log2(e) is exactly 2^-3, bf16(c q) = q / 8 is exact and the
+    result is softmax(q k^T / 8 ln 2) v; with 1/sqrt(128) the rounding of c q
+    makes it differ from fp32_qk, by little."""
+    gen = torch.Generator().manual_seed(31)
+    q, k, v = (torch.randn(1, 2, 40, 128, generator=gen).to(BF) for _ in range(3))
+    log2e = np.float32(1.4426950408889634)
+    s = np.float32(0.125 / 1.4426950408889634)
+    while np.float32(s * log2e) != np.float32(0.125):
+        s = np.nextafter(s, np.float32(1.0) if np.float32(s * log2e) < 0.125 else np.float32(0.0))
+    pre = o.attention_bf16_prescale(q, k, v, float(s))
+    assert (pre - o.attention(q, k, v, 0.125 * math.log(2.0))).abs().max().item() < 1e-12
+    pre = o.attention_bf16_prescale(q, k, v, 128 ** -0.5)
+    d = (pre - o.attention(q, k, v, 128 ** -0.5)).abs().max().item()
+    assert 0 < d < 1e-2
