@@ -54,6 +54,18 @@ NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothed
                                            NineToothedTensor k, NineToothedTensor v,
                                            NineToothedTensor scale, NineToothedTensor o);
 
+/* The same operator built for head dim 72 (the Qwen vision tower's heads):
+ * q, o: [B, H, Sq, 72]; k, v: [B, H, Sk, 72]; otherwise as
+ * launch_h3_full_attention (fp32_qk numerics). Returns an error for any other
+ * head dim, as launch_h3_full_attention does for a head dim other than 128.
+ * Replaces launch_h3_vision_attention_72 (scripts/build_h3_attention.py:23-24,
+ * tools/h3_attention.py:104-121 with head_dim=72; called at
+ * patches/InfiniCore.patch:1421-1423 when q's head dim is 72, allowed by
+ * :1376 under H3_QWEN_NINETOOTHED=1). */
+NineToothedResult launch_h3_vision_attention_72(NineToothedStream stream, NineToothedTensor q,
+                                                NineToothedTensor k, NineToothedTensor v,
+                                                NineToothedTensor scale, NineToothedTensor o);
+
 /* The `bf16_prescale` numerics of the same operator: q enters the product as
  * bf16(fp32(scale * log2(e)) * q) and the logits are used as they come
  * (tools/h3_attention.py:87-101, selected by make_attention(numerics=

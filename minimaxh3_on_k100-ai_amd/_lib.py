@@ -19,6 +19,7 @@ LIBRARY_PATH = Path(__file__).resolve().parent / "libh3mi355x.so"
 # Entry points and their NineToothedTensor argument counts (stream excluded).
 ENTRY_POINTS = {
     "launch_h3_full_attention": 5,
+    "launch_h3_vision_attention_72": 5,
     "launch_h3_full_attention_bf16_prescale": 5,
     "launch_h3_full_attention_fp8": 8,
     "launch_h3_full_attention_fp8pv": 6,

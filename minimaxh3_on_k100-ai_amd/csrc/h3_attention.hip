@@ -73,6 +73,9 @@ struct AttnArgs {
 // The dword-3 word of a raw buffer descriptor on gfx9 (CDNA): no format
 // conversion, bounds checked against num_records in bytes.
 constexpr int kBufferWord3 = 0x00020000;
+// A per-lane buffer offset past any descriptor range here (ranges and tile
+// offsets stay below 2^31, so offset + tile offset cannot wrap).
+constexpr int kBeyondRange = 0x40000000;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -91,14 +94,19 @@ __device__ __forceinline__ int xcd_remap(int x, int total) {
 // (their scores become -inf and their probabilities exactly 0, which leaves
 // the finite V rows without effect). The registers are native vectors, so
 // the copies stay in registers.
+// DIM < 128: the head's dims past DIM are zero in the tile (the 16-byte chunks
+// past DIM / 8 read the row's last chunk and are replaced by zeros).
+template <int DIM>
 __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid,
                                           u32x4_t (&reg)[kLoadRows]) {
     const int t = threadIdx.x;
+    const int chunk = t % 16, cc = chunk < DIM / 8 ? chunk : DIM / 8 - 1;
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r) {
         const int row0 = t / 16 + (kThreadsWG / 16) * r;
         const int row = row0 < valid ? row0 : valid - 1;
-        reg[r] = *reinterpret_cast<const u32x4_t *>(base + static_cast<int64_t>(key0 + row) * s_stride + (t % 16) * 8);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t *>(base + static_cast<int64_t>(key0 + row) * s_stride + cc * 8);
+        reg[r] = chunk < DIM / 8 ? v : u32x4_t{0u, 0u, 0u, 0u};
     }
 }
 
@@ -247,8 +255,11 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 }
 
 // BUF: K and V tiles through buffer loads (the host checks that one head's
-// rows fit a 31-bit byte range and that rows do not overlap).
-template <bool NEG, bool BUF>
+// rows fit a 31-bit byte range and that rows do not overlap). DIM: the head
+// dim, 128 or 72; a 72-dim head runs as a 128-dim one whose dims 72..127 are
+// zero in Q, K and V (the dot products and the first 72 output dims are those
+// of the 72-dim head) and only dims 0..71 are stored.
+template <bool NEG, bool BUF, int DIM>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElemsK];
     __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElemsV];
@@ -277,9 +288,14 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     for (int qs = 0; qs < kQS; ++qs) {
         int query = q_first + qs * 32 + l32;
         query = query < a.Sq ? query : a.Sq - 1;
-        const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2] + 8 * half;
+        const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) qreg[qs][kk] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 16 * kk));
+        for (int kk = 0; kk < 8; ++kk) {
+            // This lane's 8 dims; past the head dim, a valid chunk is read and zeroed.
+            const int d0 = 16 * kk + 8 * half;
+            const uint4 u = *reinterpret_cast<const uint4 *>(qrow + (d0 < DIM ? d0 : DIM - 8));
+            qreg[qs][kk] = as_bf16x8(d0 < DIM ? u : make_uint4(0u, 0u, 0u, 0u));
+        }
         if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
@@ -321,14 +337,16 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         for (int r = 0; r < kLoadRows; ++r) {
             const int row = static_cast<int>(threadIdx.x) / 16 + (kThreadsWG / 16) * r;
             const int chunk = static_cast<int>(threadIdx.x) % 16 * 8;
-            kvoff[r] = (row * static_cast<int>(a.ks[2]) + chunk) * 2;
-            vvoff[r] = (row * static_cast<int>(a.vs[2]) + chunk) * 2;
+            // Chunks past the head dim point past the descriptor's range (which
+            // is below 2^31 with every tile offset) and read as zero.
+            kvoff[r] = chunk < DIM ? (row * static_cast<int>(a.ks[2]) + chunk) * 2 : kBeyondRange;
+            vvoff[r] = chunk < DIM ? (row * static_cast<int>(a.vs[2]) + chunk) * 2 : kBeyondRange;
         }
         load_tile_buf(krs, kvoff, 0, kreg);
         load_tile_buf(vrs, vvoff, 0, vreg);
     } else {
-        load_tile(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
-        load_tile(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+        load_tile<DIM>(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
+        load_tile<DIM>(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
     }
     store_tile<kRowK>(lds_k[0], kreg);
     store_tile<kRowV>(lds_v[0], vreg);
@@ -359,8 +377,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
             // they need no branch either.
             const int n0 = has_next ? next0 : a.Sk - 1;
             const int nvalid = a.Sk - n0 < kBN ? a.Sk - n0 : kBN;
-            load_tile(kbase, a.ks[2], n0, nvalid, kreg);
-            load_tile(vbase, a.vs[2], n0, nvalid, vreg);
+            load_tile<DIM>(kbase, a.ks[2], n0, nvalid, kreg);
+            load_tile<DIM>(vbase, a.vs[2], n0, nvalid, vreg);
         }
         attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, c_loop, krow, half, v_row_off,
                                 v_col_off);
@@ -391,7 +409,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
                 uint2 w;
                 w.x = pack2(acc[db][qs][4 * g + 0] * inv, acc[db][qs][4 * g + 1] * inv);
                 w.y = pack2(acc[db][qs][4 * g + 2] * inv, acc[db][qs][4 * g + 3] * inv);
-                *reinterpret_cast<uint2 *>(orow + 32 * db + 8 * g + 4 * half) = w;
+                if (32 * db + 8 * g + 4 * half < DIM) *reinterpret_cast<uint2 *>(orow + 32 * db + 8 * g + 4 * half) = w;
             }
     }
 }
@@ -406,17 +424,18 @@ namespace {
 // The launcher of both numerics: fp32_qk (logits scaled by c = scale log2 e in
 // fp32) and bf16_prescale (q rounded to bf16(c q) before the product).
 int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedTensor k, NineToothedTensor v,
-                     NineToothedTensor scale, NineToothedTensor o, bool prescale) {
+                     NineToothedTensor scale, NineToothedTensor o, bool prescale, int64_t dim) {
     View<4> qv, kv, vv, ov;
     double sc;
     if (!load_view(q, 2, qv) || !load_view(k, 2, kv) || !load_view(v, 2, vv) || !load_view(o, 2, ov) ||
         !load_scalar(scale, sc))
         return kInvalid;
     // Contract of the reference operator (patches/InfiniCore.patch:1366-1376):
-    // same B/H/D, q and o alike, k and v alike, Sq and Sk free; here D = 128.
+    // same B/H/D, q and o alike, k and v alike, Sq and Sk free; D = `dim`
+    // (128, or 72 for the vision launcher).
     if (!same_shape(qv, ov) || !same_shape(kv, vv)) return kInvalid;
     if (qv.shape[0] != kv.shape[0] || qv.shape[1] != kv.shape[1] || qv.shape[3] != kv.shape[3]) return kInvalid;
-    if (qv.shape[3] != kD) return kInvalid;
+    if (qv.shape[3] != dim) return kInvalid;
     if (!rows_vec16(qv, 2) || !rows_vec16(kv, 2) || !rows_vec16(vv, 2) || !rows_vec16(ov, 2)) return kInvalid;
     if (qv.shape[0] == 0 || qv.shape[1] == 0 || qv.shape[2] == 0) return 0;
     if (kv.shape[2] == 0) return kInvalid;  // softmax over no keys is undefined
@@ -444,27 +463,22 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
     // past the end, which the last iteration's unused loads reach) fit a
     // 31-bit byte range and rows do not overlap.
     auto extent = [&](int64_t stride) -> int64_t {
-        return stride >= kD ? (static_cast<int64_t>(a.Sk) - 1) * stride * 2 + kD * 2 : -1;
+        return stride >= dim ? (static_cast<int64_t>(a.Sk) - 1) * stride * 2 + dim * 2 : -1;
     };
     const int64_t k_ext = extent(a.ks[2]), v_ext = extent(a.vs[2]);
     const int64_t reach = (static_cast<int64_t>(a.Sk) + 2 * kBN) * 2 *
                           (a.ks[2] > a.vs[2] ? a.ks[2] : a.vs[2]);
-    const bool buf = k_ext > 0 && v_ext > 0 && reach < (int64_t{1} << 31);
+    const bool buf = k_ext > 0 && v_ext > 0 && reach < (int64_t{1} << 30);
     a.k_bytes = buf ? static_cast<int>(k_ext) : 0;
     a.v_bytes = buf ? static_cast<int>(v_ext) : 0;
     const unsigned g = static_cast<unsigned>(grid);
     hipStream_t st = as_stream(stream);
-    if (a.c < 0.0f && !prescale) {  // the loop's max runs over c * s
-        if (buf)
-            attention_fwd_kernel<true, true><<<g, kThreadsWG, 0, st>>>(a);
-        else
-            attention_fwd_kernel<true, false><<<g, kThreadsWG, 0, st>>>(a);
-    } else {
-        if (buf)
-            attention_fwd_kernel<false, true><<<g, kThreadsWG, 0, st>>>(a);
-        else
-            attention_fwd_kernel<false, false><<<g, kThreadsWG, 0, st>>>(a);
-    }
+    const bool neg = a.c < 0.0f && !prescale;  // the loop's max runs over c * s
+#define H3_ATTN(N, B, D) \
+    if (neg == N && buf == B && dim == D) attention_fwd_kernel<N, B, D><<<g, kThreadsWG, 0, st>>>(a);
+    H3_ATTN(false, true, 128) H3_ATTN(false, false, 128) H3_ATTN(true, true, 128) H3_ATTN(true, false, 128)
+    H3_ATTN(false, true, 72) H3_ATTN(false, false, 72) H3_ATTN(true, true, 72) H3_ATTN(true, false, 72)
+#undef H3_ATTN
     return launch_status();
 }
 
@@ -473,11 +487,17 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
 extern "C" NineToothedResult launch_h3_full_attention(NineToothedStream stream, NineToothedTensor q,
                                                       NineToothedTensor k, NineToothedTensor v,
                                                       NineToothedTensor scale, NineToothedTensor o) {
-    return launch_attention(stream, q, k, v, scale, o, false);
+    return launch_attention(stream, q, k, v, scale, o, false, kD);
+}
+
+extern "C" NineToothedResult launch_h3_vision_attention_72(NineToothedStream stream, NineToothedTensor q,
+                                                           NineToothedTensor k, NineToothedTensor v,
+                                                           NineToothedTensor scale, NineToothedTensor o) {
+    return launch_attention(stream, q, k, v, scale, o, false, 72);
 }
 
 extern "C" NineToothedResult launch_h3_full_attention_bf16_prescale(NineToothedStream stream, NineToothedTensor q,
                                                                     NineToothedTensor k, NineToothedTensor v,
                                                                     NineToothedTensor scale, NineToothedTensor o) {
-    return launch_attention(stream, q, k, v, scale, o, true);
+    return launch_attention(stream, q, k, v, scale, o, true, kD);
 }

@@ -14,7 +14,9 @@ Numerics (tools/h3_attention.py:25-101):
     the last key tile is masked, so the three coincide.
   - "bf16_prescale" (:87-101): q enters the product as bf16(fp32(scale log2 e) q)
     and the logits are used unscaled (launch_h3_full_attention_bf16_prescale).
-Only head_dim 128 (the DiT's) is built; D = 72 (Qwen vision) is not.
+head_dim 128 (the DiT's) and 72 (the Qwen vision tower's, launcher
+launch_h3_vision_attention_72 as in scripts/build_h3_attention.py:23-24) are
+built; as in the reference, a factory runs only tensors of its own head_dim.
 
 fp8 (no counterpart in the reference): `quantize_fp8_per_head` (per-head
 absmax e4m3fn codes), `make_attention_fp8` (Q K^T and P.V on the fp8 MFMA)
@@ -46,17 +48,24 @@ def make_attention(block_m=128, block_n=32, num_warps=4, num_stages=1, caller="t
                    head_dim=128, dtype=None):
     if head_dim <= 0:
         raise ValueError("head_dim must be positive")
-    if head_dim != 128:
-        raise ValueError(f"the gfx950 attention kernel is built for head_dim 128, got {head_dim}")
+    if head_dim not in (128, 72):
+        raise ValueError(f"the gfx950 attention kernel is built for head_dim 128 and 72, got {head_dim}")
+    if head_dim == 72 and numerics == "bf16_prescale":
+        raise ValueError("bf16_prescale is built for head_dim 128 only")
     if numerics not in NUMERICS:
         raise ValueError(f"Unknown attention numerics: {numerics}")
     if dtype is not None and str(getattr(dtype, "name", dtype)).lower() not in ("bfloat16", "torch.bfloat16", "bf16"):
         raise ValueError(f"only the bfloat16 attention kernel is built, got dtype={dtype!r}")
 
-    entry = "launch_h3_full_attention_bf16_prescale" if numerics == "bf16_prescale" else "launch_h3_full_attention"
+    if head_dim == 72:
+        entry = "launch_h3_vision_attention_72"
+    else:
+        entry = "launch_h3_full_attention_bf16_prescale" if numerics == "bf16_prescale" else "launch_h3_full_attention"
 
     def kernel(q, k, v, scale, out):
         _check_qkvo(q, k, v, out)
+        if q.shape[3] != head_dim:
+            raise ValueError(f"this kernel is built for head_dim {head_dim}, got tensors of head dim {q.shape[3]}")
         device = _lib.check_cuda(q, k, v, out)
         _lib.check_dtype(torch.bfloat16, q, k, v, out)
         _lib.launch(entry, device, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.scalar(scale),

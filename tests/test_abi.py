@@ -159,6 +159,15 @@ CASES = [
     ("launch_h3_full_attention", [t([1 << 16, 1 << 12, 1 << 20, 128]), t([1 << 16, 1 << 12, 8, 128]),
                                   t([1 << 16, 1 << 12, 8, 128]), scal(0.1), t([1 << 16, 1 << 12, 1 << 20, 128])],
      "grid above 2^31"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 72])] * 3 + [scal(0.1), t([1, 2, 8, 72])], "head dim 72 on the 128 launcher"),
+    ("launch_h3_vision_attention_72", [t([1, 2, 8, 128])] * 3 + [scal(0.1), t([1, 2, 8, 128])],
+     "head dim 128 on the 72 launcher"),
+    ("launch_h3_vision_attention_72", [t([1, 2, 8, 72]), t([1, 2, 9, 72]), t([1, 2, 8, 72]), scal(0.1),
+                                       t([1, 2, 8, 72])], "vision k/v length mismatch"),
+    ("launch_h3_vision_attention_72", [t([1, 2, 8, 72], [1152, 576, 72, 2])] + [t([1, 2, 8, 72])] * 2
+     + [scal(0.1), t([1, 2, 8, 72])], "vision non-unit head-dim stride"),
+    ("launch_h3_vision_attention_72", [t([1, 2, 8, 72]), t([1, 2, 0, 72]), t([1, 2, 0, 72]), scal(0.1),
+                                       t([1, 2, 8, 72])], "vision no keys"),
 ]
 
 
@@ -187,6 +196,8 @@ EMPTY = [
                                       t([0, 48]), t([0])] + [t([0, 2, 3, 128])] * 3),
     ("launch_h3_full_attention", [t([1, 2, 0, 128]), t([1, 2, 8, 128]), t([1, 2, 8, 128]), scal(0.1),
                                   t([1, 2, 0, 128])]),
+    ("launch_h3_vision_attention_72", [t([1, 2, 0, 72]), t([1, 2, 8, 72]), t([1, 2, 8, 72]), scal(0.1),
+                                       t([1, 2, 0, 72])]),
 ]
 
 
@@ -202,6 +213,9 @@ def test_python_factories_validate(pkg):
         pkg.make_attention(head_dim=64)
     with pytest.raises(ValueError):
         pkg.make_attention(head_dim=0)
+    with pytest.raises(ValueError):
+        pkg.make_attention(head_dim=72, numerics="bf16_prescale")
+    pkg.make_attention(head_dim=72)
     with pytest.raises(ValueError):
         pkg.make_attention(numerics="tf32")
     with pytest.raises(ValueError):

@@ -129,6 +129,67 @@ def test_attention_scale_edge_cases(pkg, oracle, device):
         assert mx <= MAX_ABS and rel <= REL_RMS, (scale, mx, rel)
 
 
+@pytest.mark.parametrize("B,H,Sq,Sk", [(1, 1, 1, 1), (2, 3, 65, 63), (1, 2, 200, 129), (2, 2, 257, 1000)])
+def test_vision_attention_72_small_vs_fp64(pkg, oracle, device, B, H, Sq, Sk):
+    """Head dim 72 (launch_h3_vision_attention_72, scripts/build_h3_attention.py:23-24)
+    in the [B, S, H, 72] layout of the reference's MHA operator."""
+    gen = torch.Generator("cpu").manual_seed(Sq * 11 + Sk)
+    q = torch.randn(B, Sq, H, 72, generator=gen).to(BF)
+    k = torch.randn(B, Sk, H, 72, generator=gen).to(BF)
+    v = torch.randn(B, Sk, H, 72, generator=gen).to(BF)
+    scale = 72 ** -0.5
+    # A sentinel past dim 72 of every output row: the kernel stores dims 0..71 only.
+    outbuf = torch.full((B, Sq, H, 80), 7.0, dtype=BF, device=device)
+    out = outbuf[..., :72]
+    pkg.make_attention(head_dim=72)(*(_bhsd(t.to(device)) for t in (q, k, v)), scale, _bhsd(out))
+    torch.cuda.synchronize()
+    ref = oracle.attention(_bhsd(q), _bhsd(k), _bhsd(v), scale)
+    mx, rel = attention_error(_bhsd(out).cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+    assert bool((outbuf[..., 72:] == 7.0).all())
+
+
+def test_vision_attention_72_packed_and_broadcast(pkg, oracle, device):
+    """Head dim 72: q, k, v as slices of one packed [1, S, 3, H, 72] tensor
+    (buffer-load path), then K / V broadcast along S (pointer path)."""
+    gen = torch.Generator("cpu").manual_seed(72)
+    S, H = 1000, 16
+    packed = torch.randn(1, S, 3, H, 72, generator=gen).to(BF)
+    pd = packed.to(device)
+    attn = pkg.make_attention(head_dim=72)
+    out = torch.empty(1, H, S, 72, dtype=BF, device=device)
+    attn(*(pd[:, :, i].transpose(1, 2) for i in range(3)), 72 ** -0.5, out)
+    torch.cuda.synchronize()
+    ref = oracle.attention(*(packed[:, :, i].transpose(1, 2) for i in range(3)), 72 ** -0.5)
+    mx, rel = attention_error(out.cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+    q = packed[:, :200, 0].transpose(1, 2)
+    krow = torch.randn(1, H, 1, 72, generator=gen).to(BF)
+    vrow = torch.randn(1, H, 1, 72, generator=gen).to(BF)
+    kd, vd = krow.to(device).expand(1, H, 333, 72), vrow.to(device).expand(1, H, 333, 72)
+    out = torch.empty(1, H, 200, 72, dtype=BF, device=device)
+    attn(q.to(device), kd, vd, 72 ** -0.5, out)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q, krow.expand(1, H, 333, 72).contiguous(), vrow.expand(1, H, 333, 72).contiguous(),
+                           72 ** -0.5)
+    mx, rel = attention_error(out.cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
+def test_vision_attention_72_s4096_vs_fp32(pkg, device):
+    """A vision-tower sized call (16 heads of 72 over 4096 patches) against the
+    chunked fp32 reference."""
+    gen = torch.Generator("cpu").manual_seed(4096)
+    q, k, v = (torch.randn(1, 4096, 16, 72, generator=gen).to(BF).to(device) for _ in range(3))
+    out = torch.empty_like(q)
+    pkg.make_attention(head_dim=72)(_bhsd(q), _bhsd(k), _bhsd(v), 72 ** -0.5, _bhsd(out))
+    torch.cuda.synchronize()
+    ref = gpu_reference_fp32(_bhsd(q), _bhsd(k), _bhsd(v), 72 ** -0.5)
+    mx, rel = attention_error(_bhsd(out), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
 def _config_check(pkg, oracle, device, S, outlier_fraction):
     q, k, v = oracle.attention_inputs(S, outlier_fraction=outlier_fraction)
     scale = 128 ** -0.5
