@@ -9,10 +9,12 @@
 //     L2 for the K/V stream;
 //   - each wave owns 32 queries and keeps its Q^T operands in registers for
 //     the whole key loop; all of a wave's state (Q, scores, O accumulators)
-//     lives in arch VGPRs (174 of the 256 a wave gets at two waves per SIMD),
+//     lives in arch VGPRs (at most the 256 a wave gets at two waves per SIMD),
 //     so the softmax never shuttles values through AGPRs;
-//   - K/V tiles of 64 keys are staged in double-buffered LDS with
-//     bank-conflict-free pitches (below).
+//   - K/V tiles of 64 keys go from HBM straight into double-buffered LDS
+//     (buffer loads with the LDS destination), in rows of 256 bytes whose
+//     16-byte chunks are XOR-swizzled so every operand read is bank-conflict
+//     free (below); the next tile's loads run during the current tile's work.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_bf16; A row = lane % 32, B column =
 // lane % 32, accumulator register i of lane l holds row 8*(i/4) + 4*(l/32) + i%4)
@@ -46,17 +48,20 @@ constexpr int kQS = 1;                        // 32-query MFMA blocks per wave
 constexpr int kThreadsWG = 64 * kWaves;
 constexpr int kBM = 32 * kQS * kWaves;        // queries per workgroup
 constexpr int kBN = 64;           // keys per tile
-// LDS row pitches (elements), chosen against 64 banks x 4 bytes:
-//   K: 272 B -> the 16 rows read by one 16-lane ds_read_b128 pass start 4
-//      banks apart and cover every bank once;
-//   V: 320 B -> the 4 rows x 16 dims of each 16-lane ds_read_b64_tr_b16
-//      group start 16 banks apart, so a 32-lane pass covers every bank once.
-constexpr int kRowK = kD + 8;
-constexpr int kRowV = kD + 32;
-constexpr int kTileElemsK = kBN * kRowK;
-constexpr int kTileElemsV = kBN * kRowV;
+// LDS tiles: 64 rows of 256 bytes (16 chunks of 8 dims), unpadded, so that a
+// wave's 64-lane buffer-to-LDS load fills 4 whole rows. The 16-byte chunk c of
+// row r sits at slot c ^ swz(r), against 64 banks x 4 bytes:
+//   K: swz(r) = r & 15 -> the 16 rows one 16-lane ds_read_b128 pass reads (same
+//      chunk) land on 16 distinct slots, every bank once;
+//   V: swz(r) = 4 (r & 3) -> each 32-lane ds_read_b64_tr_b16 pass reads 4 rows
+//      x 4 chunks, 16 distinct slots, every bank once.
+constexpr int kRow = kD;
+constexpr int kTileElems = kBN * kRow;
 constexpr int kLoadRows = kBN * 16 / kThreadsWG;  // 16-byte chunks per thread per tile
 static_assert(kBN * 16 % kThreadsWG == 0, "a tile is an exact number of chunks per thread");
+static_assert(kLoadRows * 64 / 16 * kWaves == kBN, "each wave's loads fill whole rows");
+__device__ __forceinline__ int swz_k(int row) { return row & 15; }
+__device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -87,54 +92,70 @@ __device__ __forceinline__ int xcd_remap(int x, int total) {
     return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
-// Global -> registers for one 64-key tile of K or V: thread t loads rows
-// t/16 + (threads/16) r, 16-byte chunk t%16. Rows past `valid` re-read row
-// valid-1: every load is issued unconditionally (a load under a branch is
-// waited for before the branch closes), and the softmax masks those keys
-// (their scores become -inf and their probabilities exactly 0, which leaves
-// the finite V rows without effect). The registers are native vectors, so
-// the copies stay in registers.
-// DIM < 128: the head's dims past DIM are zero in the tile (the 16-byte chunks
-// past DIM / 8 read the row's last chunk and are replaced by zeros).
-template <int DIM>
+// Thread t's share of a 64-key tile: wave w's i-th load (i < kLoadRows) fills
+// tile rows 4 (kLoadRows w + i) .. +3, one row per 16 lanes; lane l fills slot
+// l % 16 of its row, which holds the row's chunk (l % 16) ^ swz(row).
+__device__ __forceinline__ int tile_row(int i) {
+    return 4 * (kLoadRows * static_cast<int>(threadIdx.x >> 6) + i) + static_cast<int>(threadIdx.x & 63) / 16;
+}
+template <bool IS_K>
+__device__ __forceinline__ int tile_chunk(int row) {
+    return static_cast<int>(threadIdx.x & 15) ^ (IS_K ? swz_k(row) : swz_v(row));
+}
+
+// Global -> registers for one 64-key tile (the pointer path). Rows past
+// `valid` re-read row valid-1: every load is issued unconditionally (a load
+// under a branch is waited for before the branch closes), and the softmax
+// masks those keys (their scores become -inf and their probabilities exactly
+// 0, which leaves the finite V rows without effect). DIM < 128: chunks past
+// DIM / 8 read the row's last chunk and are replaced by zeros.
+template <bool IS_K, int DIM>
 __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid,
                                           u32x4_t (&reg)[kLoadRows]) {
-    const int t = threadIdx.x;
-    const int chunk = t % 16, cc = chunk < DIM / 8 ? chunk : DIM / 8 - 1;
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r) {
-        const int row0 = t / 16 + (kThreadsWG / 16) * r;
+        const int row0 = tile_row(r);
         const int row = row0 < valid ? row0 : valid - 1;
+        const int chunk = tile_chunk<IS_K>(row0), cc = chunk < DIM / 8 ? chunk : DIM / 8 - 1;
         const u32x4_t v = *reinterpret_cast<const u32x4_t *>(base + static_cast<int64_t>(key0 + row) * s_stride + cc * 8);
         reg[r] = chunk < DIM / 8 ? v : u32x4_t{0u, 0u, 0u, 0u};
     }
 }
 
-// The same tile through buffer loads: per-thread byte offsets fixed for the
-// kernel (voff) plus the tile's uniform byte offset (soff). Rows past the
-// head's last key fall outside the descriptor's range and read as zero
-// (their scores are masked), so no address is clamped and no VALU is spent on
-// addresses per tile.
-__device__ __forceinline__ void load_tile_buf(__amdgpu_buffer_rsrc_t rs, const int (&voff)[kLoadRows], int soff,
-                                              u32x4_t (&reg)[kLoadRows]) {
-#pragma unroll
-    for (int r = 0; r < kLoadRows; ++r) reg[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[r], soff, 0);
-}
-
-template <int PITCH>
+// Registers -> the LDS tile: load r of wave w is one contiguous 1 KiB run.
 __device__ __forceinline__ void store_tile(bf16_t *lds, const u32x4_t (&reg)[kLoadRows]) {
-    const int t = threadIdx.x;
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r)
-        *reinterpret_cast<u32x4_t *>(lds + (t / 16 + (kThreadsWG / 16) * r) * PITCH + (t % 16) * 8) = reg[r];
+        *reinterpret_cast<u32x4_t *>(lds + 4 * kRow * (kLoadRows * static_cast<int>(threadIdx.x >> 6) + r) +
+                                     8 * static_cast<int>(threadIdx.x & 63)) = reg[r];
+}
+
+// Global -> LDS directly (the buffer path): each buffer load writes lane l's
+// 16 bytes at the wave's LDS base + 16 l, with per-thread byte offsets fixed
+// for the kernel (voff) plus the tile's uniform byte offset (soff). Rows past
+// the head's last key fall outside the descriptor's range and read as zero
+// (their scores are masked), so no address is clamped per tile. The loads
+// complete asynchronously: the caller waits on vmcnt before the barrier that
+// publishes the tile.
+__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rs, const int (&voff)[kLoadRows], int soff,
+                                         bf16_t *lds) {
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+#pragma unroll
+    for (int r = 0; r < kLoadRows; ++r)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void *)(lds + 4 * kRow * (kLoadRows * w + r)), 16, voff[r], soff, 0,
+            0);
 }
 
 // One 64-key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK marks the
 // last, partial tile (keys >= valid are excluded).
+// kidx: element index of this lane's K operand chunk for k-step 0 (k-step kk
+// is kidx ^ 16 kk); vidx: of its V^T operand for dim block 0 (block db is
+// vidx ^ 32 db).
 template <bool MASK, bool NEG>
 __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[kQS][8],
                                             f32x16_t (&acc)[4][kQS], float (&m_run)[kQS], float (&l_run)[kQS], float c,
-                                            int krow, int half, int v_row_off, int v_col_off) {
+                                            int kidx, int half, int vidx) {
     f32x16_t s[2][kQS];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -144,8 +165,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
             for (int i = 0; i < 16; ++i) s[ks][qs][i] = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-            const bf16x8_t kop =
-                as_bf16x8(*reinterpret_cast<const uint4 *>(kt + (32 * ks + krow) * kRowK + 16 * kk + 8 * half));
+            const bf16x8_t kop = as_bf16x8(*reinterpret_cast<const uint4 *>(kt + 32 * ks * kRow + (kidx ^ (16 * kk))));
 #pragma unroll
             for (int qs = 0; qs < kQS; ++qs)
                 s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qreg[qs][kk], s[ks][qs], 0, 0, 0);
@@ -233,9 +253,9 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            const bf16_t *vp = vt + (16 * t + v_row_off) * kRowV + 32 * db + v_col_off;
+            const bf16_t *vp = vt + 16 * t * kRow + (vidx ^ (32 * db));
             const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp));
-            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRowV));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRow));
             const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
             const bf16x8_t vop = as_bf16x8(make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
 #pragma unroll
@@ -261,8 +281,13 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 // of the 72-dim head) and only dims 0..71 are stored.
 template <bool NEG, bool BUF, int DIM>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) bf16_t lds_k[2][kTileElemsK];
-    __shared__ __attribute__((aligned(16))) bf16_t lds_v[2][kTileElemsV];
+    // Two buffers per operand as separate arrays: the loads into one buffer
+    // then provably do not alias the reads of the other, so the compiler's
+    // wait for the loads is not placed before those reads.
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_k0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_k1[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_v0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_v1[kTileElems];
 
     const int total = a.B * a.H * a.qblocks;
     const int logical = xcd_remap(blockIdx.x, total);
@@ -335,63 +360,76 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     if constexpr (BUF) {
 #pragma unroll
         for (int r = 0; r < kLoadRows; ++r) {
-            const int row = static_cast<int>(threadIdx.x) / 16 + (kThreadsWG / 16) * r;
-            const int chunk = static_cast<int>(threadIdx.x) % 16 * 8;
+            const int row = tile_row(r);
+            const int kc = 8 * tile_chunk<true>(row), vc = 8 * tile_chunk<false>(row);
             // Chunks past the head dim point past the descriptor's range (which
             // is below 2^31 with every tile offset) and read as zero.
-            kvoff[r] = chunk < DIM ? (row * static_cast<int>(a.ks[2]) + chunk) * 2 : kBeyondRange;
-            vvoff[r] = chunk < DIM ? (row * static_cast<int>(a.vs[2]) + chunk) * 2 : kBeyondRange;
+            kvoff[r] = kc < DIM ? (row * static_cast<int>(a.ks[2]) + kc) * 2 : kBeyondRange;
+            vvoff[r] = vc < DIM ? (row * static_cast<int>(a.vs[2]) + vc) * 2 : kBeyondRange;
         }
-        load_tile_buf(krs, kvoff, 0, kreg);
-        load_tile_buf(vrs, vvoff, 0, vreg);
+        dma_tile(krs, kvoff, 0, lds_k0);
+        dma_tile(vrs, vvoff, 0, lds_v0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
-        load_tile<DIM>(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
-        load_tile<DIM>(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+        load_tile<true, DIM>(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
+        load_tile<false, DIM>(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+        store_tile(lds_k0, kreg);
+        store_tile(lds_v0, vreg);
     }
-    store_tile<kRowK>(lds_k[0], kreg);
-    store_tile<kRowV>(lds_v[0], vreg);
     __syncthreads();
 
-    // K row read by MFMA row m (bits 2 and 3 swapped).
+    // This lane's K operand: row pi(l32) of each 32-key block (MFMA row m reads
+    // K row pi(m), bits 2 and 3 swapped), chunk 2 kk + half at slot
+    // (2 kk + half) ^ swz_k(row), i.e. element index kidx ^ 16 kk.
     const int krow = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int kidx = krow * kRow + 8 * (half ^ swz_k(krow));
     // ds_read_b64_tr_b16 addressing for the V^T operand: within each 16-lane
-    // group, lane s points at row (s/4) and dims 4*(s%4) of its 4x16 block.
+    // group, lane s points at row (s/4) and dims 4*(s%4) of its 4x16 block;
+    // dims 32 db + col sit at element (32 db + col) ^ 8 swz_v(row) of the row.
     const int g16 = lane >> 4, s16 = lane & 15;
     const int v_row_off = 8 * (g16 >> 1) + (s16 >> 2);
     const int v_col_off = 16 * (g16 & 1) + 4 * (s16 & 3);
+    const int vidx = v_row_off * kRow + (v_col_off ^ (8 * swz_v(v_row_off)));
 
     // The logits' factor: c, or 1 when c is already in bf16(c q).
     const float c_loop = a.prescale ? 1.0f : a.c;
-    // Full tiles in the loop; a partial last tile (Sk % 64 != 0) after it.
-    const int full = a.Sk / kBN;
-    for (int tile = 0; tile < full; ++tile) {
-        const int buf = tile & 1;
+    // One full tile from (kc, vc) while the next is loaded into (kn, vn).
+    auto step = [&](int tile, const bf16_t *kc, const bf16_t *vc, bf16_t *kn, bf16_t *vn) {
         const int next0 = (tile + 1) * kBN;
         const bool has_next = next0 < a.Sk;
         if constexpr (BUF) {
-            // After the last tile the loads fall past the rows and read zeros (unused).
-            load_tile_buf(krs, kvoff, (tile + 1) * kstep, kreg);
-            load_tile_buf(vrs, vvoff, (tile + 1) * vstep, vreg);
+            // After the last tile the loads fall past the rows and write zeros (unused).
+            dma_tile(krs, kvoff, (tile + 1) * kstep, kn);
+            dma_tile(vrs, vvoff, (tile + 1) * vstep, vn);
         } else {
             // After the last tile the loads re-read the last row (unused), so
             // they need no branch either.
             const int n0 = has_next ? next0 : a.Sk - 1;
             const int nvalid = a.Sk - n0 < kBN ? a.Sk - n0 : kBN;
-            load_tile<DIM>(kbase, a.ks[2], n0, nvalid, kreg);
-            load_tile<DIM>(vbase, a.vs[2], n0, nvalid, vreg);
+            load_tile<true, DIM>(kbase, a.ks[2], n0, nvalid, kreg);
+            load_tile<false, DIM>(vbase, a.vs[2], n0, nvalid, vreg);
         }
-        attend_tile<false, NEG>(lds_k[buf], lds_v[buf], kBN, qreg, acc, m_run, l_run, c_loop, krow, half, v_row_off,
-                                v_col_off);
-        if (has_next) {
-            store_tile<kRowK>(lds_k[buf ^ 1], kreg);
-            store_tile<kRowV>(lds_v[buf ^ 1], vreg);
+        attend_tile<false, NEG>(kc, vc, kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
+        if constexpr (BUF) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else if (has_next) {
+            store_tile(kn, kreg);
+            store_tile(vn, vreg);
         }
         __syncthreads();
+    };
+    // Full tiles in the loop, two per iteration (the buffers alternate); a
+    // partial last tile (Sk % 64 != 0) after it.
+    const int full = a.Sk / kBN;
+    for (int tile = 0; tile < full; tile += 2) {
+        step(tile, lds_k0, lds_v0, lds_k1, lds_v1);
+        if (tile + 1 < full) step(tile + 1, lds_k1, lds_v1, lds_k0, lds_v0);
     }
     if (full * kBN < a.Sk) {
-        const int buf = full & 1;
-        attend_tile<true, NEG>(lds_k[buf], lds_v[buf], a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, krow, half,
-                               v_row_off, v_col_off);
+        if (full & 1)
+            attend_tile<true, NEG>(lds_k1, lds_v1, a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
+        else
+            attend_tile<true, NEG>(lds_k0, lds_v0, a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
     }
 
     // ---- o = acc / denominator, bf16; lane owns one query, dims
