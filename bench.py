@@ -129,6 +129,14 @@ def bench_pointwise(pkg, device) -> dict:
     nbytes = 2 * T * H * 128 * 2 + T * 48 * 2 * 2 + 128 * 2
     ms = time_graph([lambda x=x, o=o: k_rh(x, w, 1e-6, table48[:, :48], table48[:, 48:], o) for x, o in zip(xs, outs)])
     record("qk_norm_rope", ms, nbytes, [T, 1, H, 128])
+    # q and k in one pass (the fused QK-RMSNorm + 3D RoPE workload: 2 x 58.7 MB
+    # of head rows + the [8192, 64] x 2 table + two weights).
+    k_qk = pkg.make_qk_norm_rope_interleaved_qk()
+    w2 = rnd(128, scale=0.1) + 1
+    nbytes = 4 * T * H * 128 * 2 + T * 64 * 2 * 2 + 2 * 128 * 2
+    ms = time_graph([lambda i=i: k_qk(xs[2 * i], xs[2 * i + 1], w, w2, 1e-6, table64[:, :64], table64[:, 64:],
+                                      outs[2 * i], outs[2 * i + 1]) for i in range(rot // 2)])
+    record("qk_norm_rope_interleaved_qk", ms, nbytes, [2, T, 1, H, 128])
     del xs, outs
     # q, k and v of one head group in one launch: by-rank views of the fused
     # [T, 3, H, 128] projection in, [1, T, H, 128] send buffers out, RoPE cache

@@ -293,6 +293,20 @@ NineToothedResult launch_h3_qk_norm_rope_interleaved(NineToothedStream stream, N
                                                      NineToothedTensor cos, NineToothedTensor sin,
                                                      NineToothedTensor out);
 
+/* launch_h3_qk_norm_rope_interleaved for q and k in ONE pass: for each
+ * (t, p, h), the q row (weight q_weight) and the k row (weight k_weight) are
+ * taken by one lane group against the same cos/sin [T, 64] entries, so the
+ * table is read once for both. q, k, q_out, k_out: bf16 [T, P, Hs, 128], any
+ * strides, all of one shape; results bitwise equal to two calls of
+ * launch_h3_qk_norm_rope_interleaved. No counterpart in the reference: it is
+ * the q+k form of the fused QK-RMSNorm + 3D RoPE workload (q and k
+ * [1, 8192, 14, 128], 32/48/48 interleaved rotary channels). */
+NineToothedResult launch_h3_qk_norm_rope_interleaved_qk(NineToothedStream stream, NineToothedTensor q,
+                                                        NineToothedTensor k, NineToothedTensor q_weight,
+                                                        NineToothedTensor k_weight, NineToothedTensor eps,
+                                                        NineToothedTensor cos, NineToothedTensor sin,
+                                                        NineToothedTensor q_out, NineToothedTensor k_out);
+
 /* H3's RoPE table: cos/sin[t, a*16 + k] = bf16(cos/sin(fp32(position[t, a]) *
  * (1 / power[k]))), position fp64 [T, 3], power fp32 [16], cos/sin bf16
  * [T, 48] views (the halves of a [T, 96] cache). Replaces launch_h3_rope_cache

@@ -21,6 +21,7 @@ from .h3_pointwise import (  # noqa: F401
     make_gated_residual_rms_modulate_indexed,
     make_qk_norm_rope,
     make_qk_norm_rope_interleaved,
+    make_qk_norm_rope_interleaved_qk,
     make_qkv_norm_rope_pack,
     make_qkv_norm_rope_pack_fp8,
     make_rms,

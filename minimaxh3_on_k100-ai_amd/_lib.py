@@ -37,6 +37,7 @@ ENTRY_POINTS = {
     "launch_h3_gated_residual_indexed": 5,
     "launch_h3_qk_norm_rope": 12,
     "launch_h3_qk_norm_rope_interleaved": 6,
+    "launch_h3_qk_norm_rope_interleaved_qk": 9,
     "launch_h3_qkv_norm_rope_pack": 12,
     "launch_h3_qkv_norm_rope_pack_fp8": 14,
     "launch_h3_rope_cache": 4,

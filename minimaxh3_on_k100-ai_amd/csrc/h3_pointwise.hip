@@ -1099,12 +1099,15 @@ struct HeadRows {
 
 struct RopeArgs {
     HeadRows x, out;
+    HeadRows x2, out2;  // a second tensor at the same (t, p, h) rows (q and k in one launch)
     const bf16_t *cos, *sin;
     int64_t cs0, cs1, ss0, ss1;  // element strides of the [T, n] cos and sin tables
     int64_t rows, P, Hs;
     FastDiv by_ph, by_h;  // row -> (t, p, h): divisions by P * Hs and by Hs
     const bf16_t *w;  // [128] RMS weight (norm kernels only)
     int64_t w_stride;
+    const bf16_t *w2;  // the second tensor's weight
+    int64_t w2_stride;
     float eps_bf;
 };
 
@@ -1324,17 +1327,20 @@ __global__ __launch_bounds__(kThreads) void head_rows_kernel(RopeArgs a) {
 // The rows of head_rows_kernel walked in batches of R rows per 16-lane group,
 // grid-strided, the next batch's x and table loads issued before the current
 // batch's arithmetic (two register sets used in turn; the loop condition is
-// uniform over the block, so no load sits under a per-lane branch).
-template <bool VEC, int MODE, int R, bool OFF32>
+// uniform over the block, so no load sits under a per-lane branch). NT = 2:
+// the group also takes the row at the same (t, p, h) of the second tensor
+// (x2 -> out2, weight w2) against the same table entries.
+template <bool VEC, int MODE, int R, bool OFF32, int NT = 1>
 __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
+    static_assert(NT == 1 || NT == 2, "one or two tensors");
     constexpr int kGroups = kThreads / 16;
     const int lane = threadIdx.x & 15;
     const uint32_t stride = gridDim.x * kGroups * R;
     const uint32_t group = threadIdx.x >> 4;
     struct Batch {
         bool ok[R];
-        int64_t out_off[R];
-        U4 xv[R];
+        int64_t out_off[R][NT];
+        U4 xv[R][NT];
         RopeTab tab[R];
     };
     auto load = [&](uint32_t block_base, Batch &bt) {
@@ -1344,27 +1350,36 @@ __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
             bt.ok[r] = row < a.rows;
             uint32_t t, p, hh;
             split_row(bt.ok[r] ? row : 0u, a.by_ph, a.by_h, t, p, hh);
-            bt.out_off[r] = head_offset<OFF32>(a.out, t, p, hh);
-            bt.xv[r] = load_head<VEC>(a.x, head_offset<OFF32>(a.x, t, p, hh), lane);
+            bt.out_off[r][0] = head_offset<OFF32>(a.out, t, p, hh);
+            bt.xv[r][0] = load_head<VEC>(a.x, head_offset<OFF32>(a.x, t, p, hh), lane);
+            if constexpr (NT == 2) {
+                bt.out_off[r][NT - 1] = head_offset<OFF32>(a.out2, t, p, hh);
+                bt.xv[r][NT - 1] = load_head<VEC>(a.x2, head_offset<OFF32>(a.x2, t, p, hh), lane);
+            }
             bt.tab[r] = load_tab<VEC, MODE, OFF32>(a, t, lane);
         }
     };
-    float w[8];
-    if constexpr (MODE != kRopeOnly) u4_to_f8(load_group<VEC>(a.w, a.w_stride, lane * 8, 128), w);
+    float w[NT][8];
+    if constexpr (MODE != kRopeOnly) {
+        u4_to_f8(load_group<VEC>(a.w, a.w_stride, lane * 8, 128), w[0]);
+        if constexpr (NT == 2) u4_to_f8(load_group<VEC>(a.w2, a.w2_stride, lane * 8, 128), w[NT - 1]);
+    }
     __shared__ bf16_t rs_tab[kRsqrtTable];
     auto finish = [&](Batch &bt) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float f[8];
-            u4_to_f8(bt.xv[r], f);
-            if constexpr (MODE != kRopeOnly) head_rms(f, w, a.eps_bf, rs_tab);
-            if constexpr (MODE == kNormRopeInterleaved) {
-                rope_interleaved(f, bt.tab[r]);
-            } else {
-                rope_rotate_half(f, lane, bt.tab[r]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                float f[8];
+                u4_to_f8(bt.xv[r][n], f);
+                if constexpr (MODE != kRopeOnly) head_rms(f, w[n], a.eps_bf, rs_tab);
+                if constexpr (MODE == kNormRopeInterleaved) {
+                    rope_interleaved(f, bt.tab[r]);
+                } else {
+                    rope_rotate_half(f, lane, bt.tab[r]);
+                }
+                if (bt.ok[r]) store_head<VEC>(n == 0 ? a.out : a.out2, bt.out_off[r][n], lane, f);
             }
-            if (bt.ok[r]) store_head<VEC>(a.out, bt.out_off[r], lane, f);
-        }
     };
     Batch A, B;
     uint32_t base = blockIdx.x * kGroups * R;
@@ -1392,15 +1407,32 @@ __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
 constexpr int kHeadLoopBlocks = 2048;
 constexpr int kHeadLoopRows = 1;
 
+// x2 / out2 / w2 (optional, all or none): a second tensor of x's shape taken
+// in the same launch (one pass over both when the rows are 16-byte aligned and
+// the offsets fit 32 bits; otherwise one launch per tensor).
 template <int MODE>
 int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, const View<2> &cos,
-                     const View<2> &sin, const View<1> *w, double eps) {
+                     const View<2> &sin, const View<1> *w, double eps, const View<4> *x2 = nullptr,
+                     const View<4> *out2 = nullptr, const View<1> *w2 = nullptr) {
     const int64_t table_width = MODE == kNormRopeInterleaved ? 64 : 48;
     if (!same_shape(x, out) || x.shape[3] != 128) return kInvalid;
     if (cos.shape[0] != x.shape[0] || cos.shape[1] != table_width || !same_shape(cos, sin)) return kInvalid;
     if (w != nullptr && w->shape[0] != 128) return kInvalid;
+    const bool pair = x2 != nullptr;
+    if (pair && (out2 == nullptr || (w == nullptr) != (w2 == nullptr) || !same_shape(*x2, x) ||
+                 !same_shape(*out2, x) || (w2 != nullptr && w2->shape[0] != 128)))
+        return kInvalid;
     bool vec = rows_vec16(x, 2) && rows_vec16(out, 2) && rows_vec16(cos, 2) && rows_vec16(sin, 2);
     if (w != nullptr) vec = vec && rows_vec16(*w, 2);
+    if (pair) {
+        const bool vec2 = vec && rows_vec16(*x2, 2) && rows_vec16(*out2, 2) && (w2 == nullptr || rows_vec16(*w2, 2));
+        const bool off2 = offsets_fit_int32(x) && offsets_fit_int32(out) && offsets_fit_int32(*x2) &&
+                          offsets_fit_int32(*out2) && offsets_fit_int32(cos) && offsets_fit_int32(sin);
+        if (!(vec2 && off2 && kHeadLoopBlocks > 0)) {
+            const int st = launch_head_rows<MODE>(stream, x, out, cos, sin, w, eps);
+            return st != 0 ? st : launch_head_rows<MODE>(stream, *x2, *out2, cos, sin, w2, eps);
+        }
+    }
     RopeArgs a{};
     a.x = {x.data, x.stride[0], x.stride[1], x.stride[2], x.stride[3]};
     a.out = {out.data, out.stride[0], out.stride[1], out.stride[2], out.stride[3]};
@@ -1422,6 +1454,14 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
         a.w = reinterpret_cast<const bf16_t *>(w->data);
         a.w_stride = w->stride[0];
     }
+    if (pair) {
+        a.x2 = {x2->data, x2->stride[0], x2->stride[1], x2->stride[2], x2->stride[3]};
+        a.out2 = {out2->data, out2->stride[0], out2->stride[1], out2->stride[2], out2->stride[3]};
+        if (w2 != nullptr) {
+            a.w2 = reinterpret_cast<const bf16_t *>(w2->data);
+            a.w2_stride = w2->stride[0];
+        }
+    }
     a.eps_bf = host_round_bf16(eps);
     if (a.rows == 0) return 0;
     // Four rows per lane group when that still leaves >= 1024 blocks.
@@ -1435,7 +1475,10 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
         constexpr int64_t kBatch = kPerBlock * kHeadLoopRows;
         const int64_t needed = (a.rows + kBatch - 1) / kBatch;
         const unsigned gl = static_cast<unsigned>(needed < kHeadLoopBlocks ? needed : kHeadLoopBlocks);
-        head_rows_loop_kernel<true, MODE, kHeadLoopRows, true><<<gl, kThreads, 0, stream>>>(a);
+        if (pair)
+            head_rows_loop_kernel<true, MODE, kHeadLoopRows, true, 2><<<gl, kThreads, 0, stream>>>(a);
+        else
+            head_rows_loop_kernel<true, MODE, kHeadLoopRows, true><<<gl, kThreads, 0, stream>>>(a);
         return launch_status();
     }
 #define H3_HEAD_ROWS(V, R, O) \
@@ -1852,6 +1895,22 @@ NineToothedResult launch_h3_qk_norm_rope_interleaved(NineToothedStream stream, N
         !load_view(weight, 2, w) || !load_scalar(eps, e))
         return kInvalid;
     return launch_head_rows<kNormRopeInterleaved>(as_stream(stream), xv, o, c, s, &w, e);
+}
+
+NineToothedResult launch_h3_qk_norm_rope_interleaved_qk(NineToothedStream stream, NineToothedTensor q,
+                                                        NineToothedTensor k, NineToothedTensor q_weight,
+                                                        NineToothedTensor k_weight, NineToothedTensor eps,
+                                                        NineToothedTensor cos, NineToothedTensor sin,
+                                                        NineToothedTensor q_out, NineToothedTensor k_out) {
+    View<4> qv, kv, qo, ko;
+    View<2> c, s;
+    View<1> wq, wk;
+    double e;
+    if (!load_view(q, 2, qv) || !load_view(k, 2, kv) || !load_view(q_out, 2, qo) || !load_view(k_out, 2, ko) ||
+        !load_view(cos, 2, c) || !load_view(sin, 2, s) || !load_view(q_weight, 2, wq) ||
+        !load_view(k_weight, 2, wk) || !load_scalar(eps, e))
+        return kInvalid;
+    return launch_head_rows<kNormRopeInterleaved>(as_stream(stream), qv, qo, c, s, &wq, e, &kv, &ko, &wk);
 }
 
 NineToothedResult launch_h3_qkv_norm_rope_pack(NineToothedStream stream, NineToothedTensor q,

@@ -17,7 +17,7 @@ from . import _lib
 __all__ = [
     "make_swiglu", "make_rms", "make_rms_modulate", "make_gated_residual",
     "make_gated_residual_rms_modulate", "make_rope", "make_qk_norm_rope",
-    "make_qk_norm_rope_interleaved", "make_rope_cache", "modulation_columns", "make_rms_modulate_indexed",
+    "make_qk_norm_rope_interleaved", "make_qk_norm_rope_interleaved_qk", "make_rope_cache", "modulation_columns", "make_rms_modulate_indexed",
     "make_gated_residual_rms_modulate_indexed", "make_gated_residual_indexed", "qkv_by_rank",
     "make_qkv_norm_rope_pack", "make_qkv_norm_rope_pack_fp8",
 ]
@@ -358,6 +358,25 @@ def make_qk_norm_rope_interleaved(dtype=None):
         device = _bf16(x, weight, cos, sin, out)
         _lib.launch("launch_h3_qk_norm_rope_interleaved", device, _lib.tensor(x), _lib.tensor(weight),
                     _lib.scalar(eps), _lib.tensor(cos), _lib.tensor(sin), _lib.tensor(out))
+
+    return launch
+
+
+def make_qk_norm_rope_interleaved_qk(dtype=None):
+    """make_qk_norm_rope_interleaved for q and k in one launch (one pass over
+    both; the table rows are read once for the two). Returns
+    launch(q, k, q_weight, k_weight, eps, cos, sin, q_out, k_out), bitwise equal
+    to the two single-tensor launches. No counterpart in the reference."""
+    _bf16_only(dtype)
+
+    def launch(q, k, q_weight, k_weight, eps, cos, sin, q_out, k_out):
+        _ndim(4, q=q, k=k, q_out=q_out, k_out=k_out)
+        _ndim(1, q_weight=q_weight, k_weight=k_weight)
+        _ndim(2, cos=cos, sin=sin)
+        device = _bf16(q, k, q_weight, k_weight, cos, sin, q_out, k_out)
+        _lib.launch("launch_h3_qk_norm_rope_interleaved_qk", device, _lib.tensor(q), _lib.tensor(k),
+                    _lib.tensor(q_weight), _lib.tensor(k_weight), _lib.scalar(eps), _lib.tensor(cos),
+                    _lib.tensor(sin), _lib.tensor(q_out), _lib.tensor(k_out))
 
     return launch
 

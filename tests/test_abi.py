@@ -140,6 +140,13 @@ CASES = [
     ("launch_h3_qkv_norm_rope_pack_fp8", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([9, 48]),
                                           t([9, 48]), t([4]), t([4, 2, 3, 64]), t([4, 2, 3, 128]),
                                           t([4, 2, 3, 128]), t([6]), t([6])], "q8 width"),
+    ("launch_h3_qk_norm_rope_interleaved_qk", [t([4, 1, 2, 128]), t([4, 1, 3, 128]), t([128]), t([128]), scal(),
+                                               t([4, 64]), t([4, 64]), t([4, 1, 2, 128]), t([4, 1, 3, 128])],
+     "q/k head counts differ"),
+    ("launch_h3_qk_norm_rope_interleaved_qk", [t([4, 1, 2, 128])] * 2 + [t([128]), t([64]), scal(), t([4, 64]),
+                                               t([4, 64])] + [t([4, 1, 2, 128])] * 2, "k weight length"),
+    ("launch_h3_qk_norm_rope_interleaved_qk", [t([4, 1, 2, 128])] * 2 + [t([128]), t([128]), scal(), t([4, 48]),
+                                               t([4, 48])] + [t([4, 1, 2, 128])] * 2, "table width 48"),
     ("launch_h3_rope_cache", [t([4, 3]), t([15]), t([4, 48]), t([4, 48])], "15 powers"),
     ("launch_h3_rope_cache", [t([4, 2]), t([16]), t([4, 48]), t([4, 48])], "2 position axes"),
     ("launch_h3_full_attention", [t([1, 2, 8, 64]), t([1, 2, 8, 64]), t([1, 2, 8, 64]), scal(0.1),

@@ -294,6 +294,34 @@ def test_qk_norm_rope_interleaved(pkg, oracle, device):
         assert_bitwise(out, oracle.qk_norm_rope_interleaved(x4, w, 1e-6, cos, sin), "interleaved")
 
 
+def test_qk_norm_rope_interleaved_qk_one_pass(pkg, oracle, device):
+    """q and k in one launch: bitwise against the oracle per tensor, on the
+    one-pass path (aligned rows) and on the two-launch fallback (head dim with
+    element stride 2), with different q / k weights and P = 2 rank-split views."""
+    q, k, w_q, w_k, pos = oracle.qk_norm_rope_inputs(T=1024, H=14, seed=4)
+    cos, sin = oracle.rope_table_interleaved(pos)
+    kern = pkg.make_qk_norm_rope_interleaved_qk()
+    q4, k4 = q[0].view(1024, 2, 7, 128), k[0].view(1024, 2, 7, 128)
+    qd, kd = q4.to(device), k4.to(device)
+    cd, sd, wqd, wkd = cos.to(device), sin.to(device), w_q.to(device), w_k.to(device)
+    refs = (oracle.qk_norm_rope_interleaved(q4, w_q, 1e-6, cos, sin),
+            oracle.qk_norm_rope_interleaved(k4, w_k, 1e-6, cos, sin))
+    qo, ko = torch.empty_like(qd), torch.empty_like(kd)
+    kern(qd, kd, wqd, wkd, 1e-6, cd, sd, qo, ko)
+    torch.cuda.synchronize()
+    assert_bitwise(qo, refs[0], "q (one pass)")
+    assert_bitwise(ko, refs[1], "k (one pass)")
+    qs = torch.zeros(1024, 2, 7, 256, dtype=BF, device=device)
+    ks = torch.zeros_like(qs)
+    qs[..., ::2] = qd
+    ks[..., ::2] = kd
+    qo2, ko2 = torch.empty_like(qd), torch.empty_like(kd)
+    kern(qs[..., ::2], ks[..., ::2], wqd, wkd, 1e-6, cd, sd, qo2, ko2)
+    torch.cuda.synchronize()
+    assert_bitwise(qo2, refs[0], "q (strided fallback)")
+    assert_bitwise(ko2, refs[1], "k (strided fallback)")
+
+
 # ------------------------------------------------------------------ RoPE table
 
 @pytest.mark.parametrize("kind", ["grid", "integer", "uniform", "fine64", "int64"])
@@ -340,6 +368,15 @@ def test_qk_norm_rope_config_size(pkg, oracle, device):
         pkg.make_qk_norm_rope()(x4.to(device), w.to(device), 1e-6, cd[:, :48], cd[:, 48:], out)
         torch.cuda.synchronize()
         assert_bitwise(out, oracle.qk_norm_rope(x4, w, 1e-6, cache[:, :48], cache[:, 48:]), "cfg rotate-half")
+    # q and k in one pass.
+    q4, k4 = q[0].view(8192, 1, 14, 128), k[0].view(8192, 1, 14, 128)
+    qo = torch.empty(8192, 1, 14, 128, dtype=BF, device=device)
+    ko = torch.empty_like(qo)
+    pkg.make_qk_norm_rope_interleaved_qk()(q4.to(device), k4.to(device), w_q.to(device), w_k.to(device), 1e-6,
+                                           cos_i.to(device), sin_i.to(device), qo, ko)
+    torch.cuda.synchronize()
+    assert_bitwise(qo, oracle.qk_norm_rope_interleaved(q4, w_q, 1e-6, cos_i, sin_i), "cfg q+k (q)")
+    assert_bitwise(ko, oracle.qk_norm_rope_interleaved(k4, w_k, 1e-6, cos_i, sin_i), "cfg q+k (k)")
 
 
 def test_chain_config_size(pkg, oracle, device):
