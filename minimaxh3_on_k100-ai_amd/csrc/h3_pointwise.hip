@@ -1403,8 +1403,10 @@ __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
 // Launch shape of head_rows_loop_kernel (the 16-byte, 32-bit-offset case):
 // blocks, and rows per 16-lane group per batch. Measured on [8192, 1, 14, 128]
 // against one batch per block: 14.8 against 16.3 us (rotate-half), 13.6
-// against 14.2 us (interleaved).
-constexpr int kHeadLoopBlocks = 2048;
+// against 14.2 us (interleaved); 4096 blocks against 2048: 24.1-25.0 against
+// 25.6-27.8 us for q and k in one launch, 13.8-14.1 against 13.9-14.5 us
+// (interleaved) and 14.4-15.0 against 15.1-16.3 us (rotate-half) per tensor.
+constexpr int kHeadLoopBlocks = 4096;
 constexpr int kHeadLoopRows = 1;
 
 // x2 / out2 / w2 (optional, all or none): a second tensor of x's shape taken
