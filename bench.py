@@ -15,7 +15,8 @@ Extra fields on the same line:
   pointwise     GB/s of each fused pointwise op at its configuration size
                 (q/k [1, 8192, 14, 128]; [8192, 7168] / [8192, 18432]), timed
                 as back-to-back launches in a HIP graph over rotating buffers
-                larger than the 256 MB last-level cache
+                larger than the 256 MB last-level cache; beside the
+                configuration ops, the reference's torch CPU path (cpu_us)
   attention_s8192, fp8   further attention configurations
 """
 from __future__ import annotations
@@ -209,6 +210,68 @@ def bench_pointwise(pkg, device) -> dict:
     return results
 
 
+def cpu_reference_path(device, pointwise: dict | None, attention_s8192: dict | None) -> None:
+    """The reference's torch CPU path beside each measured op: the oracle's
+    restatement of the torch compositions (order="torch", the literal eager
+    sums; tools/bench_h3_ops.py:81-113,145-149,215,232-234,251-254) at the
+    configuration sizes, once each after a small warm-up, on this host's
+    threads; and the fp32 attention at S = 8192, H = 14. Adds "cpu_us" /
+    "cpu_GB/s" (same algorithmic bytes as the GPU figure) to the pointwise
+    entries and "cpu_TFLOP/s" to the S = 8192 line. Inputs are drawn on the
+    GPU from a seeded generator and copied to the host (same shapes and
+    distributions as the GPU runs)."""
+    from oracle import h3_oracle
+    gen = torch.Generator(device=device).manual_seed(1)
+    bf = torch.bfloat16
+
+    def rnd(*shape, scale=1.0, offset=0.0):
+        return (torch.randn(*shape, generator=gen, device=device) * scale + offset).to(bf).cpu()
+
+    def timed(fn) -> float:
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    threads = torch.get_num_threads()
+    h3_oracle.rms_modulate(rnd(1, 64, 7168), rnd(7168), 1e-6, rnd(1, 1, 7168), rnd(1, 1, 7168), order="torch")
+
+    def note(name, seconds):
+        if pointwise is None or name not in pointwise:
+            return
+        entry = pointwise[name]
+        entry["cpu_us"] = round(seconds * 1e6, 1)
+        entry["cpu_GB/s"] = round(entry["bytes"] / seconds / 1e9, 2)
+        log(f"  cpu {name:30s} {seconds * 1e3:9.1f} ms  {entry['cpu_GB/s']:7.2f} GB/s  ({threads} threads)")
+
+    if pointwise is not None:
+        T, H = 8192, 14
+        q, k = rnd(T, 1, H, 128), rnd(T, 1, H, 128)
+        wq, wk = rnd(128, scale=0.1, offset=1.0), rnd(128, scale=0.1, offset=1.0)
+        cos, sin = h3_oracle.rope_table_interleaved(h3_oracle.grid_positions(8, 32, 32))
+        note("qk_norm_rope_interleaved_qk", timed(lambda: [h3_oracle.qk_norm_rope_interleaved(
+            x, w, 1e-6, cos, sin, order="torch") for x, w in ((q, wq), (k, wk))]))
+        del q, k
+        S, C, F = 8192, 7168, 18432
+        x, y = rnd(1, S, C), rnd(1, S, C)
+        w = rnd(C, scale=0.1, offset=1.0)
+        scale, shift, gate = (rnd(1, 1, C, scale=0.1) for _ in range(3))
+        note("rms_modulate", timed(lambda: h3_oracle.rms_modulate(x, w, 1e-6, scale, shift, order="torch")))
+        note("gated_residual", timed(lambda: h3_oracle.gated_residual(x, gate, y)))
+        note("gated_residual_rms_modulate", timed(lambda: h3_oracle.gated_residual_rms_modulate(
+            x, gate, y, w, 1e-6, scale, shift, order="torch")))
+        del x, y
+        up, gact = rnd(1, S, F), rnd(1, S, F)
+        note("swiglu", timed(lambda: h3_oracle.swiglu(up, gact)))
+        del up, gact
+    if attention_s8192 is not None:
+        S2, H = 8192, 14
+        q, k, v = (rnd(1, H, S2, 128) for _ in range(3))
+        seconds = timed(lambda: h3_oracle.attention(q, k, v, 128 ** -0.5, dtype=torch.float32, chunk=2048))
+        attention_s8192["cpu_TFLOP/s"] = round(4.0 * H * S2 * S2 * 128 / seconds / 1e12, 4)
+        attention_s8192["cpu_threads"] = threads
+        log(f"  cpu attention S={S2}: {seconds:.2f} s, {attention_s8192['cpu_TFLOP/s']} TFLOP/s ({threads} threads)")
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     """The CPU oracle's fp32 attention (softmax(q k^T s) v, chunked 2048 query
     rows) on heads of the S = 73,984, H = 14 workload, head after head until
@@ -346,6 +409,8 @@ def main() -> int:
         log("cpu baseline (oracle fp32 attention on the host)...")
         line["cpu_baseline"] = cpu_baseline()
         log(f"  {line['cpu_baseline']}")
+        log("reference torch CPU path beside each op...")
+        cpu_reference_path(device, line.get("pointwise"), line.get("attention_s8192"))
 
     print(json.dumps(line), flush=True)
     return 0

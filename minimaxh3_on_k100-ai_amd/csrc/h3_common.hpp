@@ -80,13 +80,15 @@ inline bool rows_vec16(const View<N> &v, int elem) {
 }
 
 // True when every element offset of the view is a non-negative value below
-// 2^31, so that kernels may form it in 32-bit arithmetic.
+// 2^31 and every stride and extent is below 2^24, so that kernels may form the
+// offsets in 32-bit arithmetic with 24-bit multiplies (v_mul_u32_u24, full
+// rate, exact while both factors are below 2^24 and the product below 2^32).
 template <int N>
 inline bool offsets_fit_int32(const View<N> &v) {
     int64_t span = 0;
     for (int i = 0; i < N; ++i) {
         if (v.shape[i] == 0) return true;
-        if (v.stride[i] < 0 || v.stride[i] >= (int64_t{1} << 31)) return false;
+        if (v.stride[i] < 0 || v.stride[i] >= (int64_t{1} << 24) || v.shape[i] >= (int64_t{1} << 24)) return false;
         span += v.stride[i] * (v.shape[i] - 1);
     }
     return span < (int64_t{1} << 31);
@@ -96,6 +98,8 @@ inline bool offsets_fit_int32(const View<N> &v) {
 // = (n * m) >> shift with m = ceil(2^(31 + s) / d), s = ceil(log2 d). The error
 // of m is below 1, so n * m / 2^(31 + s) exceeds n / d by less than
 // n / 2^(31 + s) < 2^-s <= 1 / d, which never reaches the next integer.
+// The device forms it as mulhi(2n, m) >> s: mulhi(2n, m) = floor(n m / 2^31)
+// (2n < 2^32), and flooring twice is flooring once by the product.
 struct FastDiv {
     uint32_t d, m, shift;
 };
@@ -107,8 +111,8 @@ inline FastDiv make_fastdiv(uint32_t d) {
     return {d, static_cast<uint32_t>(m), 31 + s};
 }
 
-__host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
-    return static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> f.shift);
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
+    return __umulhi(n << 1, f.m) >> (f.shift - 31);
 }
 
 // True when a byte view has unit inner stride and every row start (and the

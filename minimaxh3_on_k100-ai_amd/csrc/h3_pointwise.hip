@@ -91,11 +91,38 @@ __device__ __forceinline__ void store8(bf16_t *row, int64_t sw, int c0, int W, c
     store_group<VEC, STREAM>(row, sw, c0, W, f8_to_u4(f));
 }
 
-// Pairwise fold of one fp32 value over groups of L lanes (L a power of two <= 64).
+// The value of lane (i - N) mod 16 of lane i's 16-lane row (DPP row_ror:N).
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Pairwise fold of one fp32 value over groups of L lanes (L a power of two <=
+// 64): stage `off` = L/2, ..., 2, 1 adds lane i ^ off to lane i (the xor
+// butterfly). For L >= 16 the stages run without LDS: off = 32 and 16 through
+// v_permlane32_swap / v_permlane16_swap (the pair's sum, in either order, is
+// v[i] + v[i ^ off] exactly), off = 8 through row_ror:8 (which is i ^ 8 within
+// a row), and off = 4, 2, 1 through row_ror:off, which equals i ^ off because
+// after the stage above the values repeat with period 2 off within the row.
 template <int L>
 __device__ __forceinline__ float fold_lanes(float v) {
+    if constexpr (L >= 16) {
+        if constexpr (L == 64) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        if constexpr (L >= 32) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        v += row_ror<8>(v);
+        v += row_ror<4>(v);
+        v += row_ror<2>(v);
+        v += row_ror<1>(v);
+    } else {
 #pragma unroll
-    for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, L);
+        for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, L);
+    }
     return v;
 }
 
@@ -1113,25 +1140,32 @@ struct RopeArgs {
 
 enum RopeMode { kRopeOnly = 0, kNormRope = 1, kNormRopeInterleaved = 2 };
 
-// Element offset of head row (t, p, hh); OFF32 when the host has checked that
-// every offset of the view is below 2^31 (offsets_fit_int32).
+// i * stride in the 32-bit offset path: the host has checked that every
+// index, stride and the divisors P * Hs and Hs are below 2^24 and every offset
+// below 2^31 (offsets_fit_int32), so the full-rate 24-bit multiply is exact.
+__device__ __forceinline__ uint32_t mul24(uint32_t i, int64_t stride) {
+    return __umul24(i, static_cast<uint32_t>(stride));
+}
+
+// Element offset of head row (t, p, hh); OFF32: the 32-bit offset path above.
 template <bool OFF32>
 __device__ __forceinline__ int64_t head_offset(const HeadRows &h, uint32_t t, uint32_t p, uint32_t hh) {
     if constexpr (OFF32) {
-        return static_cast<int64_t>(t * static_cast<uint32_t>(h.s0) + p * static_cast<uint32_t>(h.s1) +
-                                    hh * static_cast<uint32_t>(h.s2));
+        return static_cast<int64_t>(mul24(t, h.s0) + mul24(p, h.s1) + mul24(hh, h.s2));
     } else {
         return static_cast<int64_t>(t) * h.s0 + static_cast<int64_t>(p) * h.s1 + static_cast<int64_t>(hh) * h.s2;
     }
 }
 
-// Row r of the [T, P, Hs] row space -> (t, p, hh), r < 2^31.
+// Row r of the [T, P, Hs] row space -> (t, p, hh), r < 2^31; OFF32: the
+// quotient-times-divisor products have 24-bit factors (checked on the host).
+template <bool OFF32>
 __device__ __forceinline__ void split_row(uint32_t r, const FastDiv &by_ph, const FastDiv &by_h, uint32_t &t,
                                           uint32_t &p, uint32_t &hh) {
     t = fast_div(r, by_ph);
-    const uint32_t rem = r - t * by_ph.d;
+    const uint32_t rem = r - (OFF32 ? __umul24(t, by_ph.d) : t * by_ph.d);
     p = fast_div(rem, by_h);
-    hh = rem - p * by_h.d;
+    hh = rem - (OFF32 ? __umul24(p, by_h.d) : p * by_h.d);
 }
 
 template <bool VEC>
@@ -1154,10 +1188,8 @@ struct RopeTab {
 template <bool VEC, int MODE, bool OFF32>
 __device__ __forceinline__ RopeTab load_tab(const RopeArgs &a, uint32_t t, int lane) {
     RopeTab tab{};
-    const bf16_t *cr = a.cos + (OFF32 ? static_cast<int64_t>(t * static_cast<uint32_t>(a.cs0))
-                                      : static_cast<int64_t>(t) * a.cs0);
-    const bf16_t *sr = a.sin + (OFF32 ? static_cast<int64_t>(t * static_cast<uint32_t>(a.ss0))
-                                      : static_cast<int64_t>(t) * a.ss0);
+    const bf16_t *cr = a.cos + (OFF32 ? static_cast<int64_t>(mul24(t, a.cs0)) : static_cast<int64_t>(t) * a.cs0);
+    const bf16_t *sr = a.sin + (OFF32 ? static_cast<int64_t>(mul24(t, a.ss0)) : static_cast<int64_t>(t) * a.ss0);
     if constexpr (MODE == kNormRopeInterleaved) {
         const int c0 = lane * 4;
         if constexpr (VEC) {
@@ -1298,7 +1330,7 @@ __global__ __launch_bounds__(kThreads) void head_rows_kernel(RopeArgs a) {
         const uint32_t row = base + r * kGroups;
         ok[r] = row < a.rows;
         uint32_t t, p, hh;
-        split_row(ok[r] ? row : 0u, a.by_ph, a.by_h, t, p, hh);
+        split_row<OFF32>(ok[r] ? row : 0u, a.by_ph, a.by_h, t, p, hh);
         out_off[r] = head_offset<OFF32>(a.out, t, p, hh);
         xv[r] = load_head<VEC>(a.x, head_offset<OFF32>(a.x, t, p, hh), lane);
         tab[r] = load_tab<VEC, MODE, OFF32>(a, t, lane);
@@ -1349,7 +1381,7 @@ __global__ __launch_bounds__(kThreads) void head_rows_loop_kernel(RopeArgs a) {
             const uint32_t row = block_base + group + r * kGroups;
             bt.ok[r] = row < a.rows;
             uint32_t t, p, hh;
-            split_row(bt.ok[r] ? row : 0u, a.by_ph, a.by_h, t, p, hh);
+            split_row<OFF32>(bt.ok[r] ? row : 0u, a.by_ph, a.by_h, t, p, hh);
             bt.out_off[r][0] = head_offset<OFF32>(a.out, t, p, hh);
             bt.xv[r][0] = load_head<VEC>(a.x, head_offset<OFF32>(a.x, t, p, hh), lane);
             if constexpr (NT == 2) {
@@ -1429,7 +1461,8 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
     if (pair) {
         const bool vec2 = vec && rows_vec16(*x2, 2) && rows_vec16(*out2, 2) && (w2 == nullptr || rows_vec16(*w2, 2));
         const bool off2 = offsets_fit_int32(x) && offsets_fit_int32(out) && offsets_fit_int32(*x2) &&
-                          offsets_fit_int32(*out2) && offsets_fit_int32(cos) && offsets_fit_int32(sin);
+                          offsets_fit_int32(*out2) && offsets_fit_int32(cos) && offsets_fit_int32(sin) &&
+                          x.shape[1] * x.shape[2] < (int64_t{1} << 24);
         if (!(vec2 && off2 && kHeadLoopBlocks > 0)) {
             const int st = launch_head_rows<MODE>(stream, x, out, cos, sin, w, eps);
             return st != 0 ? st : launch_head_rows<MODE>(stream, *x2, *out2, cos, sin, w2, eps);
@@ -1451,7 +1484,7 @@ int launch_head_rows(hipStream_t stream, const View<4> &x, const View<4> &out, c
     a.by_ph = make_fastdiv(static_cast<uint32_t>(a.P * a.Hs > 0 ? a.P * a.Hs : 1));
     a.by_h = make_fastdiv(static_cast<uint32_t>(a.Hs > 0 ? a.Hs : 1));
     const bool off32 = offsets_fit_int32(x) && offsets_fit_int32(out) && offsets_fit_int32(cos) &&
-                       offsets_fit_int32(sin);
+                       offsets_fit_int32(sin) && a.P * a.Hs < (int64_t{1} << 24);
     if (w != nullptr) {
         a.w = reinterpret_cast<const bf16_t *>(w->data);
         a.w_stride = w->stride[0];
@@ -1581,13 +1614,13 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
             const uint32_t row = tile * kGroups * R + group + r * kGroups;
             bt.ok[r] = row < a.rows;
             uint32_t p, hh;
-            split_row(bt.ok[r] ? row : 0u, a.by_ph, a.by_h, t[r], p, hh);
+            split_row<OFF32>(bt.ok[r] ? row : 0u, a.by_ph, a.by_h, t[r], p, hh);
             bt.out_off[r] = head_offset<OFF32>(out, t[r], p, hh);
             bt.xv[r] = load_head<VEC>(in, head_offset<OFF32>(in, t[r], p, hh), lane);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int64_t m = a.pos[OFF32 ? static_cast<int64_t>(t[r] * static_cast<uint32_t>(a.pos_stride))
+            const int64_t m = a.pos[OFF32 ? static_cast<int64_t>(mul24(t[r], a.pos_stride))
                                            : static_cast<int64_t>(t[r]) * a.pos_stride];
             const uint32_t row = static_cast<uint32_t>(m < 0 ? 0 : (m < a.table_rows ? m : a.table_rows - 1));
             bt.tab[r] = load_tab<VEC, kNormRope, OFF32>(ta, row, lane);
@@ -1728,7 +1761,8 @@ int launch_qkv_pack(hipStream_t stream, const View<4> *in, const View<4> *out, c
     if (rows >= (int64_t{1} << 31) - kThreads * 4) return kInvalid;
     a.by_ph = make_fastdiv(static_cast<uint32_t>(a.P * a.Hs));
     a.by_h = make_fastdiv(static_cast<uint32_t>(a.Hs));
-    bool off32 = offsets_fit_int32(cos) && offsets_fit_int32(sin) && offsets_fit_int32(pos);
+    bool off32 = offsets_fit_int32(cos) && offsets_fit_int32(sin) && offsets_fit_int32(pos) &&
+                 a.P * a.Hs < (int64_t{1} << 24);
     for (int i = 0; i < 3; ++i) off32 = off32 && offsets_fit_int32(in[i]) && offsets_fit_int32(out[i]);
     // kQkvBlocks blocks per tensor at most, one batch of kThreads / 16 rows each
     // per turn.

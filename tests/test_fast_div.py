@@ -1,6 +1,7 @@
 """The launch-time division of the head-row kernels (FastDiv in
 csrc/h3_common.hpp): q = (n * m) >> (31 + s), m = ceil(2^(31 + s) / d),
-s = ceil(log2 d), claimed exact for every n < 2^31. Checked against integer
+s = ceil(log2 d), claimed exact for every n < 2^31, and formed on the device as
+mulhi(2n, m) >> s (mulhi: the high 32 bits of the 64-bit product). Checked against integer
 division over every divisor up to 4096 plus large ones, at the dividends where
 an error would first show (just below and at each multiple of d near 2^31,
 and small n). CPU only."""
@@ -17,7 +18,9 @@ def magic(d: int):
 
 
 def fast_div(n: int, m: int, shift: int) -> int:
-    return ((n * m) & ((1 << 64) - 1)) >> shift  # the device's 64-bit product
+    assert 0 <= n < (1 << 31) and shift >= 31
+    mulhi = ((n << 1) * m) >> 32  # v_mul_hi_u32 of 2n (< 2^32) and m
+    return mulhi >> (shift - 31)
 
 
 def test_magic_fits_32_bits_and_divides_exactly():
