@@ -294,6 +294,40 @@ def test_qk_norm_rope_interleaved(pkg, oracle, device):
         assert_bitwise(out, oracle.qk_norm_rope_interleaved(x4, w, 1e-6, cos, sin), "interleaved")
 
 
+@pytest.mark.parametrize("stride", [(1 << 24) - 128, (1 << 24) + 128])
+def test_head_rows_token_stride_near_2_24(pkg, oracle, device, stride):
+    """Token strides on both sides of the head-row kernels' 32-bit offset
+    limit (strides below 2^24, offsets below 2^31: 24-bit multiplies): just
+    below it the largest offset is 127 x (2^24 - 128) + 1791, about 2^31 -
+    1.7e7; just above it the launch takes the 64-bit offset path. One tensor
+    and q + k in one launch, bitwise against the oracle."""
+    T, H = 128, 14
+    q, k, w_q, w_k, pos = oracle.qk_norm_rope_inputs(T=T, H=H, seed=11)
+    cos, sin = oracle.rope_table_interleaved(pos)
+    cd, sd = cos.to(device), sin.to(device)
+    refs = (oracle.qk_norm_rope_interleaved(q[0].view(T, 1, H, 128), w_q, 1e-6, cos, sin),
+            oracle.qk_norm_rope_interleaved(k[0].view(T, 1, H, 128), w_k, 1e-6, cos, sin))
+
+    def strided(src):
+        buf = torch.empty(T, stride, dtype=BF, device=device)
+        if src is not None:
+            buf[:, :H * 128] = src.reshape(T, H * 128).to(device)
+        return buf, buf[:, :H * 128].view(T, 1, H, 128)
+
+    qbuf, qv = strided(q)
+    obuf, ov = strided(None)
+    pkg.make_qk_norm_rope_interleaved()(qv, w_q.to(device), 1e-6, cd, sd, ov)
+    torch.cuda.synchronize()
+    assert_bitwise(ov.cpu(), refs[0], f"q, token stride {stride}")
+    kbuf, kv = strided(k)
+    o2buf, o2v = strided(None)
+    pkg.make_qk_norm_rope_interleaved_qk()(qv, kv, w_q.to(device), w_k.to(device), 1e-6, cd, sd, ov, o2v)
+    torch.cuda.synchronize()
+    assert_bitwise(ov.cpu(), refs[0], f"q of q + k, token stride {stride}")
+    assert_bitwise(o2v.cpu(), refs[1], f"k of q + k, token stride {stride}")
+    del qbuf, obuf, kbuf, o2buf
+
+
 def test_qk_norm_rope_interleaved_qk_one_pass(pkg, oracle, device):
     """q and k in one launch: bitwise against the oracle per tensor, on the
     one-pass path (aligned rows) and on the two-launch fallback (head dim with
