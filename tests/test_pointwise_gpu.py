@@ -55,6 +55,9 @@ RMS_CASES = [
     (2, 129, 5376, "packed_offset"),      # inner stride 1, rows not 16-byte aligned -> generic path
     (2, 129, 7168, "packed_aligned"),     # strided rows, 16-byte aligned -> vector path
     (1, 33, 72, "contiguous"),
+    (1, 65, 200, "contiguous"),           # 25 groups -> 32-lane rows (lane fold from xor 16)
+    (2, 33, 384, "contiguous"),           # 48 groups -> 64-lane rows (lane fold from xor 32)
+    (1, 31, 256, "packed_aligned"),       # exactly 32 lanes of one group each
     (1, 33, 100, "contiguous"),           # W % 8 != 0 -> generic path
     (1, 17, 1000, "transposed"),          # non-unit inner stride
     (1, 5, 8, "contiguous"),
@@ -129,7 +132,8 @@ def test_gated_residual(pkg, oracle, device, B, S, W, broadcast_gate):
     assert_bitwise(out, torch.add(x, torch.mul(gate, y)), "gated_residual vs torch bf16 ops")
 
 
-@pytest.mark.parametrize("B,S,W", [(1, 257, 5376), (2, 65, 7168), (1, 33, 100), (1, 64, 128), (3, 19, 2048)])
+@pytest.mark.parametrize("B,S,W", [(1, 257, 5376), (2, 65, 7168), (1, 33, 100), (1, 64, 128), (3, 19, 2048),
+                                   (1, 65, 200), (2, 33, 384)])
 @pytest.mark.parametrize("broadcast", [False, True])
 def test_gated_residual_rms_modulate(pkg, oracle, device, B, S, W, broadcast):
     gen = _gen(7 * W + S)
