@@ -181,6 +181,7 @@ struct RmsArgs {
     float eps_bf;  // eps already rounded fp64 -> fp32 -> bf16
     bool staged;   // weight, scale, shift and gate are the same for every s of a batch entry
     ModIndex index;  // gate, scale and shift rows per token (indexed entry points)
+    FastDiv by_s;    // row -> (b, s): division by S (rows < 2^31)
 };
 
 // bf16(1 + scale) of a group: the modulation factor, packed.
@@ -479,16 +480,21 @@ __global__ __launch_bounds__(THREADS) void rms_staged_kernel(RmsArgs a) {
 // RMSNorm + AdaLN with per-token modulation rows (ModIndex), W8 <= 64 * G:
 // rms_staged_kernel's order and register use over all B * S rows. A block
 // takes groups of kWaves consecutive rows, one per wave, the groups
-// grid-strided. The weight is staged once. Every wave reads all kWaves
-// indices of its group (the same values, so every wave takes the same
-// branches below): when they name one table row -- nearly every group, the
-// indices coming in long runs -- that row's factor and shift are staged in LDS
-// unless they are there already; a group across a run boundary reads each
-// row's factor and shift from the tables (L2) instead. The launch bound keeps
-// two blocks resident per CU up to G = 14 (W = 7168).
+// grid-strided. The weight is staged once. Lane j < kWaves of every wave
+// splits row j of the group into (b, s) with the launch-time division by S and
+// loads that row's index (lanes past kWaves repeat them), before the wave's
+// own row is loaded, so the index arrives first. One ballot tells every wave
+// whether the group's kWaves indices name one table row -- nearly every group,
+// the indices coming in long runs -- and each wave takes its own (b, s) and
+// index from lane `wave`. All waves therefore take the same branches: a group
+// of one table row stages that row's factor and shift in LDS unless they are
+// there already; a group across a run boundary reads each row's factor and
+// shift from the tables (L2) instead. The launch bound keeps two blocks
+// resident per CU up to G = 14 (W = 7168).
 template <int G, int THREADS>
 __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed_kernel(RmsArgs a) {
     constexpr int kWaves = THREADS / 64;
+    static_assert((kWaves & (kWaves - 1)) == 0 && kWaves <= 64, "a power-of-two number of waves");
     extern __shared__ U4 staged[];
     const int W8 = (a.W + 7) / 8;
     U4 *lw = staged, *lk = staged + W8, *lsh = staged + 2 * W8;
@@ -496,6 +502,7 @@ __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t step = static_cast<int64_t>(gridDim.x) * kWaves;
     const int64_t last = a.rows - 1;
+    const uint32_t S32 = static_cast<uint32_t>(a.S);
     U4 v[G];
     auto load_row = [&](int64_t b, int64_t s) {
 #pragma unroll
@@ -506,52 +513,36 @@ __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed
     for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWaves; base < a.rows; base += step) {
         // same trip count in every wave
         const bool ok = base + wave < a.rows;
-        // Coordinates of the group's rows (rows past the end repeat the last
-        // row), walked from one division. The wave's own row is loaded first,
-        // then the group's indices, whose wait overlaps the row's; no load
-        // sits under a branch, which would wait for it at the branch's end.
-        int64_t bw[kWaves], sw[kWaves], m[kWaves], b = 0, s = 0;
-        {
-            const int64_t i0 = base < last ? base : last;
-            bw[0] = i0 / a.S;
-            sw[0] = i0 % a.S;
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) {
-                const bool wrap = base + w <= last && sw[w - 1] + 1 == a.S;
-                bw[w] = wrap ? bw[w - 1] + 1 : bw[w - 1];
-                sw[w] = wrap ? 0 : (base + w <= last ? sw[w - 1] + 1 : sw[w - 1]);
-            }
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                b = w == wave ? bw[w] : b;
-                s = w == wave ? sw[w] : s;
-            }
-        }
+        // Row j of the group in lane j (rows past the end repeat the last
+        // row): (b, s) and its index; no load sits under a branch.
+        const int64_t rj64 = base + (lane & (kWaves - 1));
+        const uint32_t rj = static_cast<uint32_t>(rj64 < last ? rj64 : last);
+        const uint32_t bj = fast_div(rj, a.by_s), sj = rj - bj * S32;
+        const int64_t mj = index_row(a.index, bj, sj);
+        const int64_t b = __builtin_amdgcn_readlane(static_cast<int>(bj), wave);
+        const int64_t s = __builtin_amdgcn_readlane(static_cast<int>(sj), wave);
         load_row(b, s);
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) m[w] = index_row_uniform(a.index, bw[w], sw[w]);
-        int64_t mine = m[0];
-        bool same = true;
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) {
-            mine = w == wave ? m[w] : mine;
-            same = same && m[w] == m[0];
-        }
+        const int64_t m0 = uniform64(mj);
+        const bool same = __builtin_amdgcn_ballot_w64(mj != m0) == 0;
+        const int64_t mine = static_cast<int64_t>(
+            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mj >> 32), wave)))
+             << 32) |
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mj), wave)));
         // Staging: the weight with the first group, the group's table row when
         // it changes. The loads go out while the row's own are in flight.
         const bool first = base == static_cast<int64_t>(blockIdx.x) * kWaves;
-        const bool restage = same && m[0] != in_lds;
+        const bool restage = same && m0 != in_lds;
         if (first || restage) {
             if (!first) __syncthreads();  // the earlier groups' reads of the staged rows are done
             for (int g = threadIdx.x; g < W8; g += THREADS) {
                 if (first) lw[g] = ld16(a.w + g * 8);
                 if (restage) {
-                    lk[g] = factor_of(ld16(row_ptr(a.scale, m[0], 0) + g * 8));
-                    lsh[g] = ld16(row_ptr(a.shift, m[0], 0) + g * 8);
+                    lk[g] = factor_of(ld16(row_ptr(a.scale, m0, 0) + g * 8));
+                    lsh[g] = ld16(row_ptr(a.shift, m0, 0) + g * 8);
                 }
             }
             __syncthreads();
-            in_lds = restage ? m[0] : in_lds;
+            in_lds = restage ? m0 : in_lds;
         }
         float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -929,6 +920,7 @@ int rms_family(int mode, hipStream_t stream, const NineToothedTensor &x_t, const
     a.w_stride = w.stride[0];
     a.rows = x.shape[0] * x.shape[1];
     a.S = x.shape[1];
+    a.by_s = make_fastdiv(static_cast<uint32_t>(a.S > 0 ? a.S : 1));
     a.W = static_cast<int>(x.shape[2]);
     a.eps_bf = host_round_bf16(eps);
     // Row-invariant within a batch entry: broadcast over S (stride 0) or S = 1.
