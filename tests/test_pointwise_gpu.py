@@ -83,7 +83,7 @@ def _layout(gen, B, S, W, layout, scale=1.0):
 
 
 @pytest.mark.parametrize("B,S,W,layout", RMS_CASES)
-@pytest.mark.parametrize("scale", [0.01, 1.0, 100.0])
+@pytest.mark.parametrize("scale", [0.01, 1.0, 100.0, 10000.0])  # tools/probe_rms_rounding.py:23
 def test_rms(pkg, oracle, device, B, S, W, layout, scale):
     gen = _gen(W + S)
     x = _layout(gen, B, S, W, layout, scale)
@@ -362,7 +362,7 @@ def test_qk_norm_rope_interleaved_qk_one_pass(pkg, oracle, device):
 
 # ------------------------------------------------------------------ RoPE table
 
-@pytest.mark.parametrize("kind", ["grid", "integer", "uniform", "fine64", "int64"])
+@pytest.mark.parametrize("kind", ["grid", "integer", "uniform", "fine", "fine64", "int64"])
 def test_rope_cache(pkg, oracle, device, kind):
     """Position sets of tools/probe_rope_cache.py:37-55; within 1 bf16 ulp of
     the oracle (device ocml vs host libm cos/sin)."""
@@ -373,6 +373,8 @@ def test_rope_cache(pkg, oracle, device, kind):
         pos = torch.randint(0, 4096, (5000, 3), generator=gen).double()
     elif kind == "uniform":
         pos = (torch.rand(5000, 3, generator=gen) * 2000 - 100).double()
+    elif kind == "fine":  # fp32 positions, widened to fp64 at the call (tools/probe_rope_cache.py:56)
+        pos = (torch.arange(15000).float().view(-1, 3) / 37).double()
     elif kind == "fine64":
         pos = torch.arange(15000).double().view(-1, 3) / 37
     else:
