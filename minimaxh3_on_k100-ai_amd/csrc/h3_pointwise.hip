@@ -1658,7 +1658,10 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
                 uint8_t *row = reinterpret_cast<uint8_t *>(out.p) + bt.out_off[r];
                 if (bt.ok[r]) {
                     if constexpr (VEC) {
-                        *reinterpret_cast<uint2 *>(row + lane * 8) = codes;
+                        // Streamed like the bf16 rows: a non-temporal 8-byte store.
+                        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                        const u32x2_t cv = {codes.x, codes.y};
+                        __builtin_nontemporal_store(cv, reinterpret_cast<u32x2_t *>(row + lane * 8));
                     } else {
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
