@@ -99,3 +99,20 @@ def test_fp8_attention_config_s73984(pkg, oracle, device, mode):
         assert rel <= 5e-2, rel
     else:
         assert rel <= 0.2, rel  # measured ~0.12: the all-fp8 recipe misses 5e-2 on this data
+
+
+@pytest.mark.parametrize("mode", ["fp8", "fp8pv"])
+@pytest.mark.parametrize("B,H,Sq,Sk", [(2, 2, 130, 333), (2, 1, 64, 65), (1, 3, 1, 100), (2, 2, 300, 64)])
+def test_fp8_attention_ragged_batched(pkg, oracle, device, mode, B, H, Sq, Sk):
+    """B > 1 and Sq != Sk (the operator contract of launch_h3_full_attention,
+    patches/InfiniCore.patch:1366-1376) on both fp8 variants, including a
+    partial last key tile, against the CPU emulation of the same algorithm."""
+    gen = torch.Generator("cpu").manual_seed(B * 1000 + Sq + Sk)
+    q = torch.randn(B, Sq, H, 128, generator=gen).to(BF).transpose(1, 2)
+    k = torch.randn(B, Sk, H, 128, generator=gen).to(BF).transpose(1, 2)
+    v = torch.randn(B, Sk, H, 128, generator=gen).to(BF).transpose(1, 2)
+    scale = 128 ** -0.5
+    out = _run(pkg, device, q, k, v, scale, mode)
+    emu = _emulated(oracle, q, k, v, scale, mode)
+    mx, rel = attention_error(out.cpu(), emu)
+    assert rel <= 1.5e-2 and mx <= 0.05, (mode, mx, rel)
