@@ -309,8 +309,9 @@ def main() -> int:
                         help="run a plain device copy of MIB MiB five times (PMC byte-counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU's share (14 heads at full sequence length); runs on more than one "
-              "GPU are not part of this build", file=sys.stderr)
+        print("bench.py measures one GPU's share (14 heads at full sequence length) on one GPU; it has no "
+              "multi-GPU mode (the path would shard by heads across GPUs, with an all-to-all either side)",
+              file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
