@@ -1,0 +1,86 @@
+"""The launchers under HIP graph capture.
+
+Every entry point runs on the caller's stream, allocates nothing and clears
+its own accumulators with a fill kernel (the fp8 quantiser's amax), so a chain
+of them can be captured once and replayed. This test captures a DiT-block
+shaped chain -- RMSNorm + AdaLN, q + k norm + RoPE, attention, the fused
+gated residual + RMSNorm + AdaLN, SwiGLU, the gated residual, and the fp8
+quantiser with the fp8 P.V attention -- in one graph, then replays it three
+times. Before each replay the inputs are rewritten by eager work on the same
+stream. Every replay is checked bitwise against the same chain run eagerly on
+those inputs into separate outputs.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import assert_bitwise
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def test_block_chain_graph_replays_match_eager(pkg, oracle, device):
+    T, H, C, F = 512, 4, 1024, 2048
+    gen = torch.Generator(device=device).manual_seed(5)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=gen, device=device) * scale).to(BF)
+
+    # Inputs rewritten before every replay (the graph reads them in place).
+    x, y, up, gact = rnd(1, T, C), rnd(1, T, C), rnd(1, T, F), rnd(1, T, F)
+    q, k, v = rnd(T, 1, H, 128), rnd(T, 1, H, 128), rnd(T, 1, H, 128)
+    w = rnd(C, scale=0.1) + 1
+    wq, wk = rnd(128, scale=0.1) + 1, rnd(128, scale=0.1) + 1
+    scale, shift, gate = (rnd(1, 1, C, scale=0.1).expand(1, T, C) for _ in range(3))
+    cos, sin = (t.to(device) for t in oracle.rope_table_interleaved(oracle.grid_positions(2, 16, 16)))
+
+    mod, qk = pkg.make_rms_modulate(), pkg.make_qk_norm_rope_interleaved_qk()
+    attn, grm = pkg.make_attention(), pkg.make_gated_residual_rms_modulate()
+    swiglu, gres = pkg.make_swiglu(), pkg.make_gated_residual()
+    fp8pv = pkg.make_attention_fp8pv()
+
+    def chain(o):
+        mod(x, w, 1e-6, scale, shift, o["mod"])
+        qk(q, k, wq, wk, 1e-6, cos, sin, o["q"], o["k"])
+        attn(o["q"].permute(1, 2, 0, 3), o["k"].permute(1, 2, 0, 3), v.permute(1, 2, 0, 3), 128 ** -0.5,
+             o["attn"].permute(1, 2, 0, 3))
+        grm(x, gate, y, w, 1e-6, scale, shift, o["res"], o["norm"])
+        swiglu(up, gact, o["act"])
+        gres(o["res"], gate, o["norm"], o["out"])
+        v8, vd = o["v8"]
+        pkg.quantize_fp8_per_head(v.permute(1, 2, 0, 3), transposed=True, x8=v8, descale=vd)
+        fp8pv(o["q"].permute(1, 2, 0, 3), o["k"].permute(1, 2, 0, 3), v8, vd, 128 ** -0.5,
+              o["attn8"].permute(1, 2, 0, 3))
+
+    def outputs():
+        o = {name: torch.empty(1, T, C, dtype=BF, device=device) for name in ("mod", "res", "norm", "out")}
+        o.update({name: torch.empty(T, 1, H, 128, dtype=BF, device=device) for name in ("q", "k", "attn", "attn8")})
+        o["act"] = torch.empty(1, T, F, dtype=BF, device=device)
+        o["v8"] = pkg.quantize_fp8_per_head(v.permute(1, 2, 0, 3), transposed=True)
+        return o
+
+    graph_out, eager_out = outputs(), outputs()
+    torch.cuda.synchronize()
+    chain(graph_out)  # warm-up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            chain(graph_out)
+    torch.cuda.synchronize()
+
+    for replay in range(3):
+        for t in (x, y, up, gact, q, k, v):
+            t.copy_(rnd(*t.shape))  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        chain(eager_out)
+        torch.cuda.synchronize()
+        for name in ("mod", "q", "k", "attn", "res", "norm", "act", "out", "attn8"):
+            assert_bitwise(graph_out[name], eager_out[name], f"replay {replay}: {name}")
+        assert torch.equal(graph_out["v8"][0].view(torch.uint8), eager_out["v8"][0].view(torch.uint8))
+        assert torch.equal(graph_out["v8"][1], eager_out["v8"][1]), f"replay {replay}: v descale"
