@@ -43,10 +43,21 @@ How each function is pinned (tests/test_oracle.py):
   attention                 float64 brute force on tiny shapes, torch SDPA,
                             invariants (key permutation, constant V, identical
                             keys -> mean V, Sk = 1, dominant key, scale 0)
+  attention_bf16_prescale   at a scale whose fp32 scale*log2(e) is 2^-3 (bf16(c q)
+                            exact) it equals fp32 attention to 1e-12; near it at
+                            1/sqrt(128)
+  rope_table_interleaved    float64 cos/sin within 1 bf16 ulp on the first and
+                            last pair of each axis; shape and axis offsets
+  quantize_fp8_per_head     the amax element of every head maps to +-448; every
+                            normal code within e4m3's 2^-4 relative step
   attention_fp8_emulated    fp32 attention: bf16 logits + fp8 P.V within
                             relative RMS 5e-2 on outlier data; the all-fp8
                             recipe within 5e-2 without outliers (no reference
                             fp8 path exists -- parity partial)
+  qkv_norm_rope_pack(_fp8)  (tests/test_qkv_pack.py) = qk_norm_rope of the cache
+                            rows gathered by position, v unchanged; the fp8
+                            bound holds on adversarial heads (one-hot, one
+                            rotated pair, several angles and weights)
 """
 from __future__ import annotations
 
