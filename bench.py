@@ -17,7 +17,7 @@ Extra fields on the same line:
                 as back-to-back launches in a HIP graph over rotating buffers
                 larger than the 256 MB last-level cache; beside the
                 configuration ops, the reference's torch CPU path (cpu_us)
-  attention_s8192, fp8   further attention configurations
+  attention_s8192, attention_d72, fp8   further attention configurations
 """
 from __future__ import annotations
 
@@ -377,6 +377,24 @@ def main() -> int:
         line["attention_s8192"] = {"ms": round(ms2, 4), "TFLOP/s": round(t2, 2),
                                    "frac": round(t2 / BF16_PEAK_TFLOPS, 4)}
         log(f"attention S={S2} H={H}: {ms2:.3f} ms, {t2:.1f} TFLOP/s")
+        del q, k, v, out
+
+    if not args.no_extra:
+        # Head dim 72 (the vision tower's attention, launch_h3_vision_attention_72):
+        # 16 heads over 4096 patches; useful flops at D = 72 (the kernel runs the
+        # head as a 128-dim one whose dims past 72 are zero).
+        S72, H72, D72 = 4096, 16, 72
+        gen72 = torch.Generator(device=device).manual_seed(0)
+        q, k, v = (torch.randn(1, S72, H72, D72, generator=gen72, device=device).to(torch.bfloat16)
+                   for _ in range(3))
+        out = torch.empty_like(q)
+        attn72 = pkg.make_attention(head_dim=D72)
+        ms72 = time_launches(lambda: attn72(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), D72 ** -0.5,
+                                            out.transpose(1, 2)), 20, 3)
+        t72 = 4.0 * S72 * S72 * D72 * H72 / (ms72 * 1e-3) / 1e12
+        line["attention_d72"] = {"ms": round(ms72, 4), "TFLOP/s": round(t72, 2), "frac": round(t72 / BF16_PEAK_TFLOPS, 4),
+                                 "shape": [1, S72, H72, D72]}
+        log(f"attention D=72 S={S72} H={H72}: {ms72:.3f} ms, {t72:.1f} TFLOP/s (useful flops at D=72)")
         del q, k, v, out
 
     if not args.no_extra:
