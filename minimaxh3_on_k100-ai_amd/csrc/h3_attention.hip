@@ -61,6 +61,13 @@ constexpr int kLoadRows = kBN * 16 / kThreadsWG;  // 16-byte chunks per thread p
 static_assert(kBN * 16 % kThreadsWG == 0, "a tile is an exact number of chunks per thread");
 static_assert(kLoadRows * 64 / 16 * kWaves == kBN, "each wave's loads fill whole rows");
 __device__ __forceinline__ int swz_k(int row) { return row & 15; }
+// The 16-dim k-steps of Q K^T and the 32-dim blocks of O^T a DIM-wide head
+// needs (dims past DIM are zero in Q, K and V): 8 and 4 at DIM = 128, 5 and 3
+// at DIM = 72.
+template <int DIM>
+constexpr int kk_steps() { return (DIM + 15) / 16; }
+template <int DIM>
+constexpr int dim_blocks() { return (DIM + 31) / 32; }
 __device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -152,7 +159,7 @@ __device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rs, const int (&
 // kidx: element index of this lane's K operand chunk for k-step 0 (k-step kk
 // is kidx ^ 16 kk); vidx: of its V^T operand for dim block 0 (block db is
 // vidx ^ 32 db).
-template <bool MASK, bool NEG>
+template <bool MASK, bool NEG, int DIM>
 __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[kQS][8],
                                             f32x16_t (&acc)[4][kQS], float (&m_run)[kQS], float (&l_run)[kQS], float c,
                                             int kidx, int half, int vidx) {
@@ -164,7 +171,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[ks][qs][i] = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
+        for (int kk = 0; kk < kk_steps<DIM>(); ++kk) {
             const bf16x8_t kop = as_bf16x8(*reinterpret_cast<const uint4 *>(kt + 32 * ks * kRow + (kidx ^ (16 * kk))));
 #pragma unroll
             for (int qs = 0; qs < kQS; ++qs)
@@ -175,7 +182,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
     // a few operands occupy VGPRs at any time.
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int i = 0; i < 14; ++i) {
+    for (int i = 0; i < 2 * kk_steps<DIM>() - 2; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, kQS, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
@@ -213,7 +220,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
             m_run[qs] = m_new;
             l_run[qs] *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+            for (int db = 0; db < dim_blocks<DIM>(); ++db)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) acc[db][qs][i] *= alpha;
         }
@@ -252,7 +259,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < dim_blocks<DIM>(); ++db) {
             const bf16_t *vp = vt + 16 * t * kRow + (vidx ^ (32 * db));
             const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp));
             const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(vp + 4 * kRow));
@@ -267,7 +274,7 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
     // operand), two operands ahead of the MFMAs.
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 14; ++i) {
+    for (int i = 0; i < 4 * dim_blocks<DIM>() - 2; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, kQS, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
@@ -276,9 +283,12 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 
 // BUF: K and V tiles through buffer loads (the host checks that one head's
 // rows fit a 31-bit byte range and that rows do not overlap). DIM: the head
-// dim, 128 or 72; a 72-dim head runs as a 128-dim one whose dims 72..127 are
-// zero in Q, K and V (the dot products and the first 72 output dims are those
-// of the 72-dim head) and only dims 0..71 are stored.
+// dim, 128 or 72. The tiles keep the 128-dim row layout; dims past DIM are
+// zero in Q, K and V, so the dot products and the first DIM output dims are
+// those of the DIM-wide head. Only the k-steps and dim blocks that hold a dim
+// below DIM are computed (72: 5 k-steps, dims 0..79, and 3 blocks, dims
+// 0..95; 22 MFMAs per tile and wave against 32), and only dims below DIM are
+// stored.
 template <bool NEG, bool BUF, int DIM>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
     // Two buffers per operand as separate arrays: the loads into one buffer
@@ -315,7 +325,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         query = query < a.Sq ? query : a.Sq - 1;
         const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
+        for (int kk = 0; kk < kk_steps<DIM>(); ++kk) {
             // This lane's 8 dims; past the head dim, a valid chunk is read and zeroed.
             const int d0 = 16 * kk + 8 * half;
             const uint4 u = *reinterpret_cast<const uint4 *>(qrow + (d0 < DIM ? d0 : DIM - 8));
@@ -323,7 +333,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         }
         if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
+            for (int kk = 0; kk < kk_steps<DIM>(); ++kk) {
                 const uint4 u = __builtin_bit_cast(uint4, qreg[qs][kk]);
                 const uint32_t w[4] = {u.x, u.y, u.z, u.w};
                 uint32_t o[4];
@@ -336,7 +346,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
 
     f32x16_t acc[4][kQS];  // O^T: dim block db (32 dims) x query block qs
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < dim_blocks<DIM>(); ++db)
 #pragma unroll
         for (int qs = 0; qs < kQS; ++qs)
 #pragma unroll
@@ -409,7 +419,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
             load_tile<true, DIM>(kbase, a.ks[2], n0, nvalid, kreg);
             load_tile<false, DIM>(vbase, a.vs[2], n0, nvalid, vreg);
         }
-        attend_tile<false, NEG>(kc, vc, kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
+        attend_tile<false, NEG, DIM>(kc, vc, kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
         if constexpr (BUF) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         } else if (has_next) {
@@ -427,9 +437,9 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     }
     if (full * kBN < a.Sk) {
         if (full & 1)
-            attend_tile<true, NEG>(lds_k1, lds_v1, a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
+            attend_tile<true, NEG, DIM>(lds_k1, lds_v1, a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
         else
-            attend_tile<true, NEG>(lds_k0, lds_v0, a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
+            attend_tile<true, NEG, DIM>(lds_k0, lds_v0, a.Sk - full * kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
     }
 
     // ---- o = acc / denominator, bf16; lane owns one query, dims
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         const float inv = __fdiv_rn(1.0f, l_run[qs]);
         bf16_t *orow = obase + static_cast<int64_t>(query) * a.os[2];
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < dim_blocks<DIM>(); ++db)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 uint2 w;
