@@ -166,6 +166,36 @@ __device__ __forceinline__ void store_v(uint8_t *lds, const u32x4_t &reg) {
     *reinterpret_cast<u32x4_t *>(lds + d * 64 + 16 * vswz(d, c)) = reg;
 }
 
+// One full K tile and V^T tile straight from HBM into LDS (the buffer path):
+// wave w's K load i and its V^T load write 64 16-byte slots each at the
+// wave's LDS base + 16 lane; `kvoff` / `vvoff` (per thread, fixed for the
+// kernel) pick the source chunk each slot holds, `ksoff` / `vsoff` are the
+// tile's uniform byte offsets. The loads complete asynchronously: the caller
+// waits on vmcnt before the barrier that publishes the tiles.
+// (Plain overloads for one and two K loads per thread: the buffer resource
+// type cannot be substituted into a template in the host pass.)
+__device__ __forceinline__ void dma_k_load(__amdgpu_buffer_rsrc_t krs, int voff, int soff, uint8_t *kn, int slot0) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void *)(kn + 16 * slot0), 16, voff,
+                                             soff, 0, 0);
+}
+__device__ __forceinline__ void dma_tile_pair(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                              const int (&kvoff)[1], int vvoff, int ksoff, int vsoff, uint8_t *kn,
+                                              uint8_t *vn) {
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    dma_k_load(krs, kvoff[0], ksoff, kn, 64 * w);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void *)(vn + 16 * 64 * w), 16,
+                                             vvoff, vsoff, 0, 0);
+}
+__device__ __forceinline__ void dma_tile_pair(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                              const int (&kvoff)[2], int vvoff, int ksoff, int vsoff, uint8_t *kn,
+                                              uint8_t *vn) {
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    dma_k_load(krs, kvoff[0], ksoff, kn, 64 * w);
+    dma_k_load(krs, kvoff[1], ksoff, kn, kThreadsWG + 64 * w);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void *)(vn + 16 * 64 * w), 16,
+                                             vvoff, vsoff, 0, 0);
+}
+
 // ------------------------------------------------------------------ kernel
 
 // BUF: the main loop's full K and V^T tiles through buffer loads, each
@@ -175,8 +205,12 @@ template <bool QK_FP8, bool NEG, bool BUF>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fp8_kernel(
     Fp8Args a) {
     constexpr int kKBytes = kBN * (QK_FP8 ? 128 : 256);
-    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kKBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kD * kBN];
+    // Two buffers per operand as separate arrays: the loads into one buffer
+    // then provably do not alias the reads of the other.
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kKBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kKBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kD * kBN];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kD * kBN];
 
     const int total = a.B * a.H * a.qblocks;
     const int logical = xcd_remap(blockIdx.x, total);
@@ -227,17 +261,15 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
         const int valid = a.Sk < kBN ? a.Sk : kBN;
         load_k<QK_FP8>(a, b, h, 0, valid, kr);
         load_v(a, b, h, 0, valid, vr);
-        store_k<QK_FP8>(lds_k[0], kr);
-        store_v(lds_v[0], vr);
+        store_k<QK_FP8>(lds_k0, kr);
+        store_v(lds_v0, vr);
     }
     __syncthreads();
 
-    // One tile of keys from LDS buffer `buf`: S^T = K Q^T, online softmax, O^T
+    // One tile of keys from the LDS tiles (kt, vt): S^T = K Q^T, online softmax, O^T
     // += V^T P^T. MASKED: keys >= valid are excluded (the last, partial tile).
-    auto attend = [&](auto masked_tag, int buf, int valid) {
+    auto attend = [&](auto masked_tag, const uint8_t *kt, const uint8_t *vt, int valid) __attribute__((always_inline)) {
         constexpr bool MASKED = decltype(masked_tag)::value;
-        const uint8_t *kt = lds_k[buf];
-        const uint8_t *vt = lds_v[buf];
 
         // ---- S^T = K Q^T: s[ks][i] = logit of key 32*half + 16*ks + i
         f32x16_t s[2];
@@ -377,35 +409,56 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                                                                          static_cast<short>(0), a.k_bytes, kBufferWord3);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(a.v8 + b * a.vs0 + h * a.vs1), static_cast<short>(0), a.v_bytes, kBufferWord3);
+    // Per-thread byte offsets of the buffer path, fixed for the kernel: wave w's
+    // load i writes tile slots 64 (8 i + w) .. +63, 16 bytes per lane, at the
+    // wave's LDS base + 16 lane (the direct-to-LDS form of the buffer load);
+    // slot s of the K tile is chunk position s % chunks of row s / chunks, so
+    // the lane loads the chunk the swizzle puts there (the swizzle is an XOR,
+    // its own inverse). Likewise slot s of the V^T tile is position s % 4 of
+    // dim row s / 4.
     int kvoff[kKPerThread], vvoff;
 #pragma unroll
     for (int i = 0; i < kKPerThread; ++i) {
-        const int idx = static_cast<int>(threadIdx.x) + i * kThreadsWG;
-        kvoff[i] = (idx / kKChunks) * static_cast<int>(k_row_bytes) + 16 * (idx % kKChunks);
+        const int slot = static_cast<int>(threadIdx.x) + i * kThreadsWG;
+        const int r = slot / kKChunks, pos = slot % kKChunks;
+        kvoff[i] = r * static_cast<int>(k_row_bytes) + 16 * (QK_FP8 ? kswz8(r, pos) : kswz16(r, pos));
     }
-    vvoff = (static_cast<int>(threadIdx.x) / 4) * static_cast<int>(a.vs3) + 16 * (static_cast<int>(threadIdx.x) % 4);
-    // Main loop: the next tile is full, so its loads need no masks or branches.
-    for (; tile + 1 < full; ++tile) {
-        const int buf = tile & 1;
-        u32x4_t kr[2], vr;
+    {
+        const int d = static_cast<int>(threadIdx.x) / 4, pos = static_cast<int>(threadIdx.x) % 4;
+        vvoff = d * static_cast<int>(a.vs3) + 16 * vswz(d, pos);
+    }
+    // One full tile from (kc, vc) while the next, also full, goes into (kn, vn).
+    auto step = [&](int t, const uint8_t *kc, const uint8_t *vc, uint8_t *kn, uint8_t *vn) {
         if constexpr (BUF) {
-            const int key1 = (tile + 1) * kBN;
-#pragma unroll
-            for (int i = 0; i < kKPerThread; ++i)
-                kr[i] = __builtin_amdgcn_raw_buffer_load_b128(krs, kvoff[i], key1 * static_cast<int>(k_row_bytes), 0);
-            vr = __builtin_amdgcn_raw_buffer_load_b128(vrs, vvoff, key1, 0);
+            dma_tile_pair(krs, vrs, kvoff, vvoff, (t + 1) * kBN * static_cast<int>(k_row_bytes),
+                                       (t + 1) * kBN, kn, vn);
+            attend(Full{}, kc, vc, kBN);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         } else {
-            load_k_full<QK_FP8>(a, b, h, (tile + 1) * kBN, kr);
-            load_v_full(a, b, h, (tile + 1) * kBN, vr);
+            u32x4_t kr[2], vr;
+            load_k_full<QK_FP8>(a, b, h, (t + 1) * kBN, kr);
+            load_v_full(a, b, h, (t + 1) * kBN, vr);
+            attend(Full{}, kc, vc, kBN);
+            store_k<QK_FP8>(kn, kr);
+            store_v(vn, vr);
         }
-        attend(Full{}, buf, kBN);
-        store_k<QK_FP8>(lds_k[buf ^ 1], kr);
-        store_v(lds_v[buf ^ 1], vr);
         __syncthreads();
+    };
+    // Main loop: the next tile is full, so its loads need no masks or branches;
+    // the buffers alternate, two tiles per iteration.
+    const int nmain = full > 1 ? full - 1 : 0;  // tiles 0 .. full-2 (their successors are full)
+    for (int t = 0; t < nmain; t += 2) {
+        step(t, lds_k0, lds_v0, lds_k1, lds_v1);
+        if (t + 1 < nmain) step(t + 1, lds_k1, lds_v1, lds_k0, lds_v0);
     }
+    tile = nmain;
     // The last full tile (if any) and the partial tile (if any).
     for (; tile < ntiles; ++tile) {
-        const int buf = tile & 1;
+        const bool odd = tile & 1;
+        const uint8_t *kc = odd ? lds_k1 : lds_k0;
+        const uint8_t *vc = odd ? lds_v1 : lds_v0;
+        uint8_t *kn = odd ? lds_k0 : lds_k1;
+        uint8_t *vn = odd ? lds_v0 : lds_v1;
         const int key0 = tile * kBN;
         const int valid = a.Sk - key0 < kBN ? a.Sk - key0 : kBN;
         const bool has_next = tile + 1 < ntiles;
@@ -416,12 +469,12 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
             load_v(a, b, h, key0 + kBN, nvalid, vr);
         }
         if (valid < kBN)
-            attend(Partial{}, buf, valid);
+            attend(Partial{}, kc, vc, valid);
         else
-            attend(Full{}, buf, kBN);
+            attend(Full{}, kc, vc, kBN);
         if (has_next) {
-            store_k<QK_FP8>(lds_k[buf ^ 1], kr);
-            store_v(lds_v[buf ^ 1], vr);
+            store_k<QK_FP8>(kn, kr);
+            store_v(vn, vr);
             __syncthreads();
         }
     }
