@@ -7,8 +7,10 @@
 //   - logits = (q8 . k8) * q_descale * k_descale * scale * log2(e) (all-fp8), or
 //     the bf16 logits of the bf16 kernel (fp8 P.V variant);
 //   - P = exp2(logit - running max) is requantised per 64-key tile as
-//     e4m3(448 * P) (P <= 1, so the fixed factor uses the whole range); the
-//     denominator sums the unquantised fp32 P; o = acc * v_descale / (448 l).
+//     e4m3(448 * P) (P <= 1, so the fixed factor uses the whole range); 448 P
+//     is formed directly as exp2(logit - (running max - log2 448)), the
+//     denominator sums the unquantised fp32 448 P, and o = acc * v_descale /
+//     denominator -- the same quantities as o = acc * v_descale / (448 l).
 //
 // Work decomposition as in the bf16 kernel: 512-thread workgroups (8 waves,
 // two per SIMD), 32 queries per wave, 64-key tiles in double-buffered LDS,
@@ -42,6 +44,7 @@ constexpr int kBM = 32 * kWaves;
 constexpr int kBN = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kE4M3Max = 448.0f;
+constexpr float kLog2E4M3Max = 8.80735492205760410744f;  // log2(448)
 constexpr int kScale1 = 127;  // E8M0 exponent of 1.0 for the scaled MFMA
 
 // ------------------------------------------------------------------ swizzles
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
     const int half = lane >> 5;
 
     const float c = QK_FP8 ? a.c * a.q_descale[h] * a.k_descale[h] : a.c;
-    const float out_scale = a.v_descale[h] / kE4M3Max;
+    const float out_scale = a.v_descale[h];  // the denominator sums 448 P
 
     // Q^T operands (this lane's query row).
     const int query = qb * kBM + wave * 32 + l32;
@@ -350,21 +353,25 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
                 for (int i = 0; i < 16; ++i) acc[db][i] *= alpha;
         }
+        // 448 P directly: exp2(logit - (m - log2 448)), one subtraction per
+        // tile instead of a multiplication per score; the denominator then
+        // sums 448 P (fp32) and the epilogue divides by it as it stands.
+        const float m_bias = m_run - kLog2E4M3Max;
         float rowsum = 0.0f;
         int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_run));
+                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_bias));
                 if (MASKED && 32 * half + 16 * ks + i >= valid) p = 0.0f;
                 s[ks][i] = p;
                 rowsum += p;
             }
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                int v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w], kE4M3Max * s[ks][4 * w + 1], 0, false);
-                v = __builtin_amdgcn_cvt_pk_fp8_f32(kE4M3Max * s[ks][4 * w + 2], kE4M3Max * s[ks][4 * w + 3], v, true);
+                int v = __builtin_amdgcn_cvt_pk_fp8_f32(s[ks][4 * w], s[ks][4 * w + 1], 0, false);
+                v = __builtin_amdgcn_cvt_pk_fp8_f32(s[ks][4 * w + 2], s[ks][4 * w + 3], v, true);
                 pk[4 * ks + w] = v;
             }
         }
