@@ -154,14 +154,6 @@ __device__ __forceinline__ int64_t index_row(const ModIndex &ix, int64_t b, int6
     const int64_t m = ix.p[b * ix.sb + s * ix.ss];
     return m < 0 ? 0 : (m < ix.count ? m : ix.count - 1);
 }
-// index_row for a (b, s) the whole wave shares, read with a scalar load (the
-// index is read-only for the kernel's lifetime): the value lands in scalar
-// registers, not in two vector registers per index.
-__device__ __forceinline__ int64_t index_row_uniform(const ModIndex &ix, int64_t b, int64_t s) {
-    typedef const __attribute__((address_space(4))) int64_t *ConstantPtr;
-    const int64_t m = *(ConstantPtr)(ix.p + b * ix.sb + s * ix.ss);
-    return m < 0 ? 0 : (m < ix.count ? m : ix.count - 1);
-}
 __device__ __forceinline__ void mod_coords(const ModIndex &ix, int64_t b, int64_t s, int64_t &mb, int64_t &ms) {
     if (ix.p == nullptr) {
         mb = b;
