@@ -8,9 +8,11 @@
 //     the bf16 logits of the bf16 kernel (fp8 P.V variant);
 //   - P = exp2(logit - running max) is requantised per 64-key tile as
 //     e4m3(448 * P) (P <= 1, so the fixed factor uses the whole range); 448 P
-//     is formed directly as exp2(logit - (running max - log2 448)), the
-//     denominator sums the unquantised fp32 448 P, and o = acc * v_descale /
-//     denominator -- the same quantities as o = acc * v_descale / (448 l).
+//     is formed directly as exp2(logit - (running max - log2 448)), and
+//     o = acc * v_descale / denominator -- the same quantities as
+//     o = acc * v_descale / (448 l). The denominator sums the fp32 448 P in
+//     the bf16-logit variant; in the all-fp8 recipe it sums the quantised
+//     e4m3(448 P) -- the weights the numerator uses -- on the MFMA.
 //
 // Work decomposition as in the bf16 kernel: 512-thread workgroups (8 waves,
 // two per SIMD), 32 queries per wave, 64-key tiles in double-buffered LDS,
@@ -45,6 +47,7 @@ constexpr int kBN = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kE4M3Max = 448.0f;
 constexpr float kLog2E4M3Max = 8.80735492205760410744f;  // log2(448)
+constexpr int kE4M3OnesX4 = 0x38383838;                   // four e4m3fn 1.0 codes
 constexpr int kScale1 = 127;  // E8M0 exponent of 1.0 for the scaled MFMA
 
 // ------------------------------------------------------------------ swizzles
@@ -257,6 +260,16 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[db][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
+    // All-fp8: the denominator on the MFMA instead (the VALU is the scarcer
+    // unit there). V^T's rows are replaced by e4m3 ones, so every accumulator
+    // register of a lane gathers its query's sum of the quantised 448 P over
+    // the keys so far; element 0 is the one the rescale keeps up to date. The
+    // bf16-logit variant keeps the fp32 sum (no VGPRs to spare).
+    f32x16_t lacc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+    const i32x8_t ones{kE4M3OnesX4, kE4M3OnesX4, kE4M3OnesX4, kE4M3OnesX4,
+                       kE4M3OnesX4, kE4M3OnesX4, kE4M3OnesX4, kE4M3OnesX4};
 
     const int ntiles = (a.Sk + kBN - 1) / kBN;
     {
@@ -347,7 +360,10 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
             const float m_new = grow ? m_tile : m_run;
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
-            l_run *= alpha;
+            if constexpr (QK_FP8)
+                lacc[0] *= alpha;
+            else
+                l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -355,7 +371,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
         }
         // 448 P directly: exp2(logit - (m - log2 448)), one subtraction per
         // tile instead of a multiplication per score; the denominator then
-        // sums 448 P (fp32) and the epilogue divides by it as it stands.
+        // sums 448 P and the epilogue divides by it as it stands.
         const float m_bias = m_run - kLog2E4M3Max;
         float rowsum = 0.0f;
         int pk[8];  // 32 e4m3 codes of 448 * P, key order 32*half + j
@@ -366,7 +382,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                 float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][i], c, -m_bias));
                 if (MASKED && 32 * half + 16 * ks + i >= valid) p = 0.0f;
                 s[ks][i] = p;
-                rowsum += p;
+                if constexpr (!QK_FP8) rowsum += p;
             }
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
@@ -375,12 +391,14 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
                 pk[4 * ks + w] = v;
             }
         }
-        {
+        const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
+        if constexpr (QK_FP8) {
+            lacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pop, lacc, 0, 0, 0, kScale1, 0, kScale1);
+        } else {
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(rowsum), __float_as_uint(rowsum), false, false);
             rowsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            l_run += rowsum;
         }
-        l_run += rowsum;
-        const i32x8_t pop{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
 
         // ---- O^T += V^T P^T, one 64-key MFMA per 32 dims
 #pragma unroll
@@ -487,7 +505,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 
     if (query >= a.Sq) return;
-    const float inv = out_scale / l_run;
+    const float inv = out_scale / (QK_FP8 ? lacc[0] : l_run);
     bf16_t *orow = a.o + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(query) * a.os[2];
 #pragma unroll
     for (int db = 0; db < 4; ++db)

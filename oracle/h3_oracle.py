@@ -415,8 +415,10 @@ def attention_fp8_emulated(q, k, v8, q_descale, k_descale, v_descale, scale: flo
     q_descale = k_descale = None (bf16 logits); v8: e4m3 codes. fp32 logits
     times q_descale*k_descale*scale*log2(e), exact running max, exp2 online
     softmax over `block_n`-key tiles, P requantised per tile to e4m3 with the
-    fixed factor 448, fp32 P.V and denominator (of the unquantised P), output
-    acc * v_descale / (448 * denominator) in bf16. [B, H, S, D]."""
+    fixed factor 448, fp32 P.V, output acc * v_descale / (448 * denominator)
+    in bf16. The denominator sums the unquantised fp32 P (bf16 logits) or, in
+    the all-fp8 recipe, the quantised weights e4m3(448 P) / 448 that the
+    numerator uses (the kernel forms that sum on the MFMA). [B, H, S, D]."""
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     qf, kf, vf = q.float(), k.float(), v8.float()
@@ -433,7 +435,7 @@ def attention_fp8_emulated(q, k, v8, q_descale, k_descale, v_descale, scale: flo
         alpha = torch.exp2(m - m_new)
         p8 = (p * E4M3_MAX).to(torch.float8_e4m3fn).float()
         acc = acc * alpha + torch.matmul(p8, vf[:, :, k0:k0 + block_n])
-        den = den * alpha + p.sum(-1, keepdim=True)
+        den = den * alpha + ((p8 / E4M3_MAX) if q_descale is not None else p).sum(-1, keepdim=True)
         m = m_new
     return (acc * v_descale.view(1, H, 1, 1) / (E4M3_MAX * den)).to(BF16)
 
