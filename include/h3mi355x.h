@@ -97,7 +97,8 @@ NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, Nine
  * o: bf16 [B, H, Sq, 128]. Logits = (q8 . k8) q_descale k_descale scale in
  * fp32 on the fp8 MFMA; P is requantised per 64-key tile to e4m3(448 P)
  * (P <= 1 after the running-max shift); the fp32 P.V accumulator is scaled by
- * v_descale / 448 and divided by the fp32 denominator.
+ * v_descale / 448 and divided by the denominator, the fp32 sum of the same
+ * quantised weights e4m3(448 P) / 448.
  * No counterpart in the reference (fp8 attention is a new feature); same
  * callers as launch_h3_full_attention. */
 NineToothedResult launch_h3_full_attention_fp8(NineToothedStream stream, NineToothedTensor q8,
