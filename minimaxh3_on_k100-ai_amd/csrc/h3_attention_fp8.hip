@@ -526,22 +526,43 @@ __global__ void zero_kernel(float *p, int n) {
     if (i < n) p[i] = 0.0f;
 }
 
-// amax[h] = max |x[:, h, :, :]|; 16 threads per 128-element row, 256 rows per block.
-__global__ __launch_bounds__(256) void amax_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2, int B, int S,
-                                                   int rows_per_block, float *amax) {
-    const int h = blockIdx.y;
-    const int64_t rows = static_cast<int64_t>(B) * S;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+// Blocks of amax_kernel over all heads: about one resident block per slot of
+// the chip. Each block folds its maxima into one atomicMax per head, so the
+// same-address device-scope atomics (serialised at the memory side) number
+// about kAmaxBlocks instead of one per 256 rows.
+constexpr int kAmaxBlocks = 2048;
+
+// amax[h] = max |x[:, h, :, :]| over the B * S rows of head h. Block j handles
+// head j % H and the 256-row chunks j / H, j / H + G, ... (G blocks per head;
+// heads vary fastest, so the blocks running together read whole token rows).
+// 16 threads per 128-element row; a thread's 16 row loads per chunk are issued
+// before its first comparison (rows past the end re-read the last row, so no
+// load sits under a branch); row r splits into (b, s) by the launch-time
+// division by S (B * S < 2^31, checked on the host).
+__global__ __launch_bounds__(256) void amax_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2, uint32_t rows,
+                                                   uint32_t chunks, int H, uint32_t G, FastDiv by_s, float *amax) {
+    constexpr int kRows = 16;
+    const int h = static_cast<int>(blockIdx.x % static_cast<uint32_t>(H));
+    const bf16_t *xh = x + h * s1 + 8 * (threadIdx.x % 16);
     uint32_t m = 0;
-    for (int64_t r = r0 + threadIdx.x / 16; r < r0 + rows_per_block && r < rows; r += 16) {
-        const int64_t bb = r / S, ss = r % S;
-        const U4 v = ld16(x + bb * s0 + h * s1 + ss * s2 + 8 * (threadIdx.x % 16));
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (uint32_t chunk = blockIdx.x / static_cast<uint32_t>(H); chunk < chunks; chunk += G) {
+        const uint32_t r0 = chunk * 256u + threadIdx.x / 16;
+        U4 v[kRows];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = (w[e] << 16) & 0x7fffffffu, hi = w[e] & 0x7fff0000u;
-            m = lo > m ? lo : m;
-            m = hi > m ? hi : m;
+        for (int i = 0; i < kRows; ++i) {
+            const uint32_t r = r0 + 16u * i < rows ? r0 + 16u * i : rows - 1;
+            const uint32_t b = fast_div(r, by_s), ss = r - b * by_s.d;
+            v[i] = ld16(xh + static_cast<int64_t>(b) * s0 + static_cast<int64_t>(ss) * s2);
+        }
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) {
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = (w[e] << 16) & 0x7fffffffu, hi = w[e] & 0x7fff0000u;
+                m = lo > m ? lo : m;
+                m = hi > m ? hi : m;
+            }
         }
     }
 #pragma unroll
@@ -549,7 +570,14 @@ __global__ __launch_bounds__(256) void amax_kernel(const bf16_t *x, int64_t s0, 
         const uint32_t o = __shfl_xor(m, off, 64);
         m = o > m ? o : m;
     }
-    if ((threadIdx.x & 63) == 0) atomicMax(reinterpret_cast<unsigned int *>(amax) + h, m);
+    __shared__ uint32_t wave_max[4];
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x / 64] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t a = wave_max[0] > wave_max[1] ? wave_max[0] : wave_max[1];
+        const uint32_t b = wave_max[2] > wave_max[3] ? wave_max[2] : wave_max[3];
+        atomicMax(reinterpret_cast<unsigned int *>(amax) + h, a > b ? a : b);
+    }
 }
 
 __device__ __forceinline__ uint32_t quant4(const float f[4], float inv) {
@@ -562,17 +590,20 @@ __device__ __forceinline__ uint32_t quant4(const float f[4], float inv) {
 }
 
 // x8 = e4m3(x * 448 / amax_h). D-contiguous output: 16 dims per thread.
+// (row, chunk) index i < 2^31 (checked on the host), split by the launch-time
+// divisions by S and H.
 __global__ __launch_bounds__(256) void quant_rows_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2,
-                                                         uint8_t *y, int64_t t0, int64_t t1, int64_t t2, int B, int H,
-                                                         int S, const float *amax) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (row, 16-dim chunk)
-    const int64_t n = static_cast<int64_t>(B) * H * S * 8;
+                                                         uint8_t *y, int64_t t0, int64_t t1, int64_t t2, uint32_t n,
+                                                         FastDiv by_s, FastDiv by_h, const float *amax) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;  // (row, 16-dim chunk)
     if (i >= n) return;
-    const int chunk = static_cast<int>(i % 8);
-    const int64_t row = i / 8;
-    const int64_t ss = row % S, bh = row / S;
-    const int hh = static_cast<int>(bh % H);
-    const int64_t bb = bh / H;
+    const int chunk = static_cast<int>(i & 7u);
+    const uint32_t row = i >> 3;
+    const uint32_t bh = fast_div(row, by_s);
+    const int64_t ss = row - bh * by_s.d;
+    const uint32_t bbu = fast_div(bh, by_h);
+    const int hh = static_cast<int>(bh - bbu * by_h.d);
+    const int64_t bb = bbu;
     const float a = amax[hh];
     const float inv = a > 0.0f ? kE4M3Max / a : 0.0f;
     const bf16_t *src = x + bb * s0 + hh * s1 + ss * s2 + 16 * chunk;
@@ -587,38 +618,84 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const bf16_t *x, int64_
     *reinterpret_cast<uint4 *>(y + bb * t0 + hh * t1 + ss * t2 + 16 * chunk) = out;
 }
 
-// x8 = e4m3(x * 448 / amax_h) written S-contiguous (V^T layout): a 64-token x
-// 128-dim tile per block, transposed through LDS.
+// 4 x 4 byte transpose: out[e] byte k = in[k] byte e. __builtin_amdgcn_perm(a,
+// b, sel) picks result byte i by selector byte i from {b bytes 0-3 as 0-3,
+// a bytes 0-3 as 4-7}.
+__device__ __forceinline__ void transpose_bytes4(const uint32_t in[4], uint32_t out[4]) {
+    const uint32_t p01 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // in0.b0 in1.b0 in0.b1 in1.b1
+    const uint32_t q01 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // in0.b2 in1.b2 in0.b3 in1.b3
+    const uint32_t p23 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+    const uint32_t q23 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+    out[1] = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
+    out[2] = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
+    out[3] = __builtin_amdgcn_perm(q23, q01, 0x07060302u);
+}
+
+// x8 = e4m3(x * 448 / amax_h) written S-contiguous (V^T layout): a 128-token x
+// 128-dim tile per block. Thread t quantises dims 8c..8c+7 (c = t % 16) of
+// tokens 4g..4g+3 and 64+4g..64+4g+3 (g = t / 16); each group of 4 tokens is
+// byte-transposed in registers into one 4-token word per dim and stored to the
+// LDS tile (128-byte rows, 16-byte pieces XOR-swizzled by (d / 8) % 8); the
+// tile leaves as 16-byte pieces, 8 per 128-byte output row. Token rows past
+// S re-read row S - 1 and are not stored.
 __global__ __launch_bounds__(256) void quant_transposed_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2,
                                                                uint8_t *y, int64_t t0, int64_t t1, int64_t t3, int H,
                                                                int S, int stiles, const float *amax) {
-    __shared__ uint8_t tile[kD][64 + 4];
+    constexpr int kTok = 128;
+    __shared__ __align__(16) uint8_t tile[kD * kTok];
     const int st = blockIdx.x % stiles;
     const int bh = blockIdx.x / stiles;
     const int hh = bh % H, bb = bh / H;
-    const int s_base = st * 64;
+    const int s_base = st * kTok;
     const float a = amax[hh];
     const float inv = a > 0.0f ? kE4M3Max / a : 0.0f;
-    // Read: 64 rows x 16 chunks of 8 dims; thread t handles chunks t, t+256, t+512, t+768.
+    const int c = threadIdx.x % 16, g = threadIdx.x / 16;
+    const bf16_t *src = x + bb * s0 + hh * s1 + 8 * c;
+    U4 v[2][4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int idx = threadIdx.x + 256 * k;
-        const int r = idx / 16, ch = idx % 16;
-        float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (s_base + r < S) u4_to_f8(ld16(x + bb * s0 + hh * s1 + static_cast<int64_t>(s_base + r) * s2 + 8 * ch), f);
-        const uint32_t lo = quant4(f, inv), hi = quant4(f + 4, inv);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            tile[8 * ch + e][r] = static_cast<uint8_t>(lo >> (8 * e));
-            tile[8 * ch + 4 + e][r] = static_cast<uint8_t>(hi >> (8 * e));
+        for (int k = 0; k < 4; ++k) {
+            const int s = min(s_base + 64 * j + 4 * g + k, S - 1);
+            v[j][k] = ld16(src + static_cast<int64_t>(s) * s2);
+        }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float f[8];
+            u4_to_f8(v[j][k], f);
+            lo[k] = quant4(f, inv);
+            hi[k] = quant4(f + 4, inv);
+        }
+        uint32_t w[8];
+        transpose_bytes4(lo, w);
+        transpose_bytes4(hi, w + 4);
+        const int piece = 4 * j + g / 4;  // 16-byte piece of the 128-token row
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int d = 8 * c + e;
+            *reinterpret_cast<uint32_t *>(tile + d * kTok + 16 * (piece ^ (c & 7)) + 4 * (g % 4)) = w[e];
         }
     }
     __syncthreads();
-    // Write: 128 dims x 64 tokens; thread t writes 32 tokens of dim t/2.
-    const int d = threadIdx.x / 2, part = threadIdx.x % 2;
-    uint8_t *dst = y + bb * t0 + hh * t1 + static_cast<int64_t>(d) * t3 + s_base + 32 * part;
-    for (int e = 0; e < 32; ++e)
-        if (s_base + 32 * part + e < S) dst[e] = tile[d][32 * part + e];
+    uint8_t *dst = y + bb * t0 + hh * t1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = threadIdx.x + 256 * i;
+        const int d = p / 8, q = p % 8;
+        const uint4 out = *reinterpret_cast<const uint4 *>(tile + d * kTok + 16 * (q ^ ((d / 8) & 7)));
+        const int s = s_base + 16 * q;
+        uint8_t *row = dst + static_cast<int64_t>(d) * t3 + s;
+        if (s + 16 <= S) {
+            *reinterpret_cast<uint4 *>(row) = out;
+        } else if (s < S) {
+            const uint32_t ww[4] = {out.x, out.y, out.z, out.w};
+            for (int e = 0; e < S - s; ++e) row[e] = static_cast<uint8_t>(ww[e / 4] >> (8 * (e % 4)));
+        }
+    }
 }
 
 // descale[h] = amax_h / 448 (1 for an all-zero head).
@@ -712,19 +789,23 @@ NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, Nine
     float *amax = reinterpret_cast<float *>(dv.data);
     zero_kernel<<<(H + 255) / 256, 256, 0, st>>>(amax, H);
     if (static_cast<int64_t>(B) * S > 0) {
-        const int rows_per_block = 256;
-        const int64_t chunks = (static_cast<int64_t>(B) * S + rows_per_block - 1) / rows_per_block;
-        if (chunks > 65535 * 1024) return kInvalid;
-        amax_kernel<<<dim3(static_cast<unsigned>(chunks), H), 256, 0, st>>>(
-            reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2], B, S, rows_per_block,
-            amax);
+        const int64_t rows = static_cast<int64_t>(B) * S;
+        const int64_t n = rows * H * 8;  // (row, 16-dim chunk) pairs of quant_rows_kernel
+        if (n >= (int64_t{1} << 31)) return kInvalid;
+        const FastDiv by_s = make_fastdiv(static_cast<uint32_t>(S)), by_h = make_fastdiv(static_cast<uint32_t>(H));
+        const int64_t chunks = (rows + 255) / 256;
+        const int64_t per = (chunks * H + kAmaxBlocks - 1) / kAmaxBlocks;  // chunks per block
+        const int64_t G = (chunks + per - 1) / per;                  // blocks per head
+        amax_kernel<<<static_cast<unsigned>(G * H), 256, 0, st>>>(
+            reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2],
+            static_cast<uint32_t>(rows), static_cast<uint32_t>(chunks), H, static_cast<uint32_t>(G), by_s, amax);
         if (d_contig) {
-            const int64_t n = static_cast<int64_t>(B) * H * S * 8;
             quant_rows_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(
                 reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2],
-                reinterpret_cast<uint8_t *>(yv.data), yv.stride[0], yv.stride[1], yv.stride[2], B, H, S, amax);
+                reinterpret_cast<uint8_t *>(yv.data), yv.stride[0], yv.stride[1], yv.stride[2],
+                static_cast<uint32_t>(n), by_s, by_h, amax);
         } else {
-            const int stiles = (S + 63) / 64;
+            const int stiles = (S + 127) / 128;
             quant_transposed_kernel<<<static_cast<unsigned>(static_cast<int64_t>(B) * H * stiles), 256, 0, st>>>(
                 reinterpret_cast<const bf16_t *>(xv.data), xv.stride[0], xv.stride[1], xv.stride[2],
                 reinterpret_cast<uint8_t *>(yv.data), yv.stride[0], yv.stride[1], yv.stride[3], H, S, stiles, amax);

@@ -49,7 +49,9 @@ How each function is pinned (tests/test_oracle.py):
   rope_table_interleaved    float64 cos/sin within 1 bf16 ulp on the first and
                             last pair of each axis; shape and axis offsets
   quantize_fp8_per_head     the amax element of every head maps to +-448; every
-                            normal code within e4m3's 2^-4 relative step
+                            normal code within e4m3's 2^-4 relative step; codes
+                            equal numpy fp32 x * (448 / amax) rounded by the
+                            e4m3 definition, on data full of exact ties
   attention_fp8_emulated    fp32 attention: bf16 logits + fp8 P.V within
                             relative RMS 5e-2 on outlier data; the all-fp8
                             recipe within 5e-2 without outliers (no reference
@@ -308,9 +310,18 @@ def qk_fp8_descale(weight: torch.Tensor) -> torch.Tensor:
     return torch.where(bound > 0, bound / E4M3_MAX, torch.ones_like(bound)), bound
 
 
+def e4m3_inverse(bound: torch.Tensor) -> torch.Tensor:
+    """fp32(448 / bound), one correctly rounded fp32 division (0 for bound 0).
+    Written as a tensor-by-tensor division: torch evaluates `scalar / tensor`
+    as reciprocal(tensor) * scalar, two roundings that can land one ulp off
+    and move an exact e4m3 tie."""
+    bound = bound.float()
+    return torch.where(bound > 0, torch.full_like(bound, E4M3_MAX) / bound, torch.zeros_like(bound))
+
+
 def quantize_fp8_with_bound(y: torch.Tensor, bound: torch.Tensor) -> torch.Tensor:
     """e4m3fn(sat(y * (448 / bound))) in fp32 (0 codes for bound 0)."""
-    inv = torch.where(bound > 0, E4M3_MAX / bound, torch.zeros_like(bound))
+    inv = e4m3_inverse(bound)
     return (y.float() * inv).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
 
 
@@ -403,7 +414,7 @@ def quantize_fp8_per_head(x: torch.Tensor):
     torch.float8_e4m3fn, descale fp32 [H])."""
     xf = x.float()
     amax = xf.abs().amax(dim=(0, 2, 3))
-    inv = torch.where(amax > 0, E4M3_MAX / amax, torch.zeros_like(amax))
+    inv = e4m3_inverse(amax)
     codes = (xf * inv.view(1, -1, 1, 1)).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
     descale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
     return codes, descale

@@ -39,6 +39,24 @@ def test_quantizer_bitwise(pkg, oracle, device, S, H, transposed):
         assert x8.stride(2) == 1
 
 
+@pytest.mark.parametrize("B,S,H,transposed", [(3, 333, 2, False), (3, 333, 2, True), (1, 40000, 14, False),
+                                               (1, 40000, 14, True)])
+def test_quantizer_bitwise_batched_and_long(pkg, oracle, device, B, S, H, transposed):
+    """B > 1 (rows split into (batch, token)) and S x H large enough that each
+    amax block folds several 256-row chunks of its head; one outlier per head
+    at a varying position sets that head's scale."""
+    gen = torch.Generator("cpu").manual_seed(B * 7 + S + H)
+    x = torch.randn(B, S, H, 128, generator=gen)
+    for h in range(H):
+        x[h % B, (h * 7919) % S, h, (h * 31) % 128] = 20.0 + h
+    x = x.to(BF).transpose(1, 2)  # [B, H, S, D] view
+    x8, d = pkg.quantize_fp8_per_head(x.to(device), transposed=transposed)
+    torch.cuda.synchronize()
+    ref8, refd = oracle.quantize_fp8_per_head(x)
+    assert torch.equal(d.cpu(), refd)
+    assert torch.equal(x8.cpu().view(torch.uint8), ref8.view(torch.uint8))
+
+
 def test_quantizer_zero_head(pkg, device):
     x = torch.zeros(1, 2, 64, 128, dtype=BF, device=device)
     x[:, 1] = 1.0

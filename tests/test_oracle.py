@@ -430,6 +430,38 @@ def test_fp8_quantisation():
     assert float(rel.max()) <= 2.0 ** -4 + 1e-6
 
 
+def _e4m3_round_nearest_even(y: np.ndarray) -> np.ndarray:
+    """e4m3fn value of fp32 y (|y| <= 448) from the format's definition: 3
+    mantissa bits, minimum normal exponent -6 (subnormal step 2^-9), ties to
+    even, in float64 where every step is exact."""
+    a = np.abs(y.astype(np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    step = np.exp2(np.maximum(e, -6.0) - 3.0)
+    return np.sign(y) * np.rint(a / step) * step
+
+
+def test_fp8_quantisation_ties_follow_a_correctly_rounded_inverse():
+    """codes = e4m3(fp32(x * fp32(448 / amax))) with one correctly rounded fp32
+    division, checked against numpy's float32 division and multiplication and
+    the definition of e4m3 rounding. amax = 23 with x multiples of 23 / 2^k
+    puts many products exactly on e4m3 ties (x = 69/64 -> 21 rounds to 20), where
+    a one-ulp error in 448 / amax moves the code."""
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(1, 3, 256, 128, generator=gen)
+    x[0, 0] = (23.0 / 64) * torch.randint(-64, 65, (256, 128), generator=gen)  # amax 23: many ties
+    x[0, 1, 0, 0] = 23.0
+    x[0, 2] *= 1e-3  # small scale: subnormal codes
+    x = x.to(torch.bfloat16)
+    x8, d = o.quantize_fp8_per_head(x)
+    xn = x.float().numpy()
+    amax = np.abs(xn).max(axis=(0, 2, 3)).astype(np.float32)
+    inv = np.float32(448.0) / amax
+    y = np.clip(xn * inv.reshape(1, -1, 1, 1), -448.0, 448.0).astype(np.float32)
+    assert np.array_equal(x8.float().numpy(), _e4m3_round_nearest_even(y))
+    assert np.array_equal(d.numpy(), amax / np.float32(448.0))
+    assert int((x8.float()[0, 0].abs() == 20.0).sum()) > 0  # the tie at 21 went to the even code
+
+
 def _fp8_case(S, outliers):
     q, k, v = o.attention_inputs(S, H=2, seed=3, outlier_fraction=outliers)
     q, k, v = (t.transpose(1, 2) for t in (q, k, v))
