@@ -83,8 +83,11 @@ NineToothedResult launch_h3_full_attention_bf16_prescale(NineToothedStream strea
  * D-contiguous (16-byte rows) or S-contiguous (the V^T layout the attention
  * kernels read V in; its D stride a multiple of 16); descale: fp32 [H]
  * (contiguous), receives amax_h / 448, the factor that maps x8 back to x.
- * A head with amax 0 gets descale 1 and all-zero codes. The kernel chain
- * clears, then accumulates, the amax in `descale` itself (no workspace).
+ * A head with amax 0 gets descale 1 and all-zero codes. Codes are
+ * e4m3fn(x * fp32(448 / amax_h)), one correctly rounded fp32 division,
+ * saturated at +-448. B * H * S * 8 < 2^31 (otherwise the invalid-argument
+ * result). The kernel chain clears, then accumulates, the amax in `descale`
+ * itself (no workspace).
  * No counterpart in the reference (it has no fp8 path); its callers are the
  * fp8 attention users below. */
 NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, NineToothedTensor x,
