@@ -531,22 +531,24 @@ __global__ void zero_kernel(float *p, int n) {
 // same-address device-scope atomics (serialised at the memory side) number
 // about kAmaxBlocks instead of one per 256 rows.
 constexpr int kAmaxBlocks = 2048;
+// Rows per thread per chunk of amax_kernel; a chunk is 16 * kAmaxRows rows.
+constexpr int kAmaxRows = 16;
 
 // amax[h] = max |x[:, h, :, :]| over the B * S rows of head h. Block j handles
-// head j % H and the 256-row chunks j / H, j / H + G, ... (G blocks per head;
+// head j % H and the chunks j / H, j / H + G, ... (G blocks per head;
 // heads vary fastest, so the blocks running together read whole token rows).
-// 16 threads per 128-element row; a thread's 16 row loads per chunk are issued
+// 16 threads per 128-element row; a thread's kAmaxRows row loads per chunk are issued
 // before its first comparison (rows past the end re-read the last row, so no
 // load sits under a branch); row r splits into (b, s) by the launch-time
 // division by S (B * S < 2^31, checked on the host).
 __global__ __launch_bounds__(256) void amax_kernel(const bf16_t *x, int64_t s0, int64_t s1, int64_t s2, uint32_t rows,
                                                    uint32_t chunks, int H, uint32_t G, FastDiv by_s, float *amax) {
-    constexpr int kRows = 16;
+    constexpr int kRows = kAmaxRows;
     const int h = static_cast<int>(blockIdx.x % static_cast<uint32_t>(H));
     const bf16_t *xh = x + h * s1 + 8 * (threadIdx.x % 16);
     uint32_t m = 0;
     for (uint32_t chunk = blockIdx.x / static_cast<uint32_t>(H); chunk < chunks; chunk += G) {
-        const uint32_t r0 = chunk * 256u + threadIdx.x / 16;
+        const uint32_t r0 = chunk * (16u * kRows) + threadIdx.x / 16;
         U4 v[kRows];
 #pragma unroll
         for (int i = 0; i < kRows; ++i) {
@@ -793,7 +795,7 @@ NineToothedResult launch_h3_quantize_fp8_per_head(NineToothedStream stream, Nine
         const int64_t n = rows * H * 8;  // (row, 16-dim chunk) pairs of quant_rows_kernel
         if (n >= (int64_t{1} << 31)) return kInvalid;
         const FastDiv by_s = make_fastdiv(static_cast<uint32_t>(S)), by_h = make_fastdiv(static_cast<uint32_t>(H));
-        const int64_t chunks = (rows + 255) / 256;
+        const int64_t chunks = (rows + 16 * kAmaxRows - 1) / (16 * kAmaxRows);
         const int64_t per = (chunks * H + kAmaxBlocks - 1) / kAmaxBlocks;  // chunks per block
         const int64_t G = (chunks + per - 1) / per;                  // blocks per head
         amax_kernel<<<static_cast<unsigned>(G * H), 256, 0, st>>>(
