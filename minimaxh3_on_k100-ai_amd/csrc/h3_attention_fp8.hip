@@ -927,7 +927,9 @@ int launch_quantize(NineToothedStream stream, const NineToothedTensor &x, const 
     }
     if (!same_shape(xv, yv) || xv.shape[3] != kD || dv.shape[0] != xv.shape[1]) return kInvalid;
     if (dv.shape[0] > 1 && dv.stride[0] != 1) return kInvalid;
-    if (amax_slots != nullptr && (sv.shape[0] != xv.shape[1] || sv.shape[1] != H3_AMAX_SLOTS || sv.stride[1] != 1))
+    // Slots are contiguous per head: H3_AMAX_SLOTS words, heads H3_AMAX_SLOTS apart.
+    if (amax_slots != nullptr && (sv.shape[0] != xv.shape[1] || sv.shape[1] != H3_AMAX_SLOTS || sv.stride[1] != 1 ||
+                                  (sv.shape[0] > 1 && sv.stride[0] != H3_AMAX_SLOTS)))
         return kInvalid;
     if (!rows_vec16(xv, 2)) return kInvalid;
     const int B = static_cast<int>(xv.shape[0]), H = static_cast<int>(xv.shape[1]), S = static_cast<int>(xv.shape[2]);

@@ -208,6 +208,10 @@ CASES = [
      "quantiser slot heads"),
     ("launch_h3_quantize_fp8_per_head_slots", [t([1, 2, 8, 128]), t([2, 64], [1, 2]), t([1, 2, 8, 128]), t([2])],
      "quantiser slots transposed"),
+    ("launch_h3_quantize_fp8_per_head_slots", [t([1, 2, 8, 128]), t([2, 64], [0, 1]), t([1, 2, 8, 128]), t([2])],
+     "quantiser slots of one head broadcast"),
+    ("launch_h3_quantize_fp8_per_head_slots", [t([1, 2, 8, 128]), t([2, 64], [128, 1]), t([1, 2, 8, 128]), t([2])],
+     "quantiser slots padded between heads"),
     ("launch_h3_quantize_fp8_per_head_slots", [t([1, 16, 1 << 24, 128]), t([16, 64]), t([1, 16, 1 << 24, 128]),
                                                t([16])], "quantiser slots 2^31 chunks"),
     ("launch_h3_qkv_norm_rope_pack_fp8_vamax", [t([4, 2, 3, 128])] * 3 + [t([128]), t([128]), scal(), t([9, 48]),

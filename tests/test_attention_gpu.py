@@ -307,6 +307,65 @@ def test_attention_reference_max_overflow_falls_back_to_exact(pkg, oracle, devic
     assert rel <= 1e-2, (case, rel)
 
 
+def _dominant_keys(Sk, keys, logit_log2, v_value):
+    """q = 16 e0 for every query, k = 0 except k[key, 0] = x at `keys`, so
+    every logit is 0 except those keys', which sit `logit_log2` log2 units
+    above (x = logit / (16 scale log2 e), exact in bf16 for the values used
+    here); v = v_value at those keys, N(0, 1) elsewhere. The fp64 reference
+    output of every query is about v_value."""
+    gen = torch.Generator("cpu").manual_seed(Sk)
+    q = torch.zeros(1, 1, 256, 128)
+    q[..., 0] = 16.0
+    k = torch.zeros(1, 1, Sk, 128)
+    k[0, 0, keys, 0] = logit_log2 / (16 * 128 ** -0.5 * math.log2(math.e))
+    v = torch.randn(1, 1, Sk, 128, generator=gen)
+    v[0, 0, keys] = v_value
+    return q.to(BF), k.to(BF), v.to(BF)
+
+
+def test_attention_folded_denominator_overflow_falls_back(pkg, oracle, device):
+    """Four keys of one later tile, one in each 16-lane group of the lanes
+    that hold a query's keys (tile offsets 0, 4, 8, 12), each 127 log2 units
+    above the first tile's maximum: every lane's partial denominator (2^127)
+    and every accumulator (4 * 2^127 * 0.25) stays finite, but the folded
+    denominator (2^129) overflows. The unit must take the exact fallback and
+    give about 0.25 everywhere, not o = 0."""
+    keys = [320, 324, 328, 332]
+    q, k, v = _dominant_keys(700, keys, 127.0, 0.25)
+    assert torch.equal(k[0, 0, keys, 0].float(), torch.full((4,), 62.25))
+    want = oracle.attention(q.double(), k.double(), v.double(), 128 ** -0.5)
+    out = torch.full(q.shape, float("nan"), dtype=BF, device=device)
+    pkg.make_attention(split_last_round=False)(q.to(device), k.to(device), v.to(device), 128 ** -0.5, out)
+    torch.cuda.synchronize()
+    mx, rel = attention_error(out.cpu(), want)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
+def test_attention_split_pieces_near_overflow_fall_back(pkg, oracle, device):
+    """A single unit split along the keys, with two keys 126.5 log2 units
+    above their piece's first tile in each of the first two pieces: each
+    piece's own denominator (about 2^127.5) is finite, but the merge's sum
+    over the pieces would overflow. A piece whose denominator or accumulators
+    exceed FLT_MAX / 8 takes the exact pass, so the merged result is finite
+    and matches the fp64 reference."""
+    Sk = 6400
+    nbytes = pkg._lib.attention_workspace_bytes(1, 1, 256, Sk)
+    split = nbytes // WS_SLOT_BYTES
+    assert split >= 2, nbytes
+    tiles = -(-Sk // 64)
+    keys = []
+    for p in range(2):
+        t = p * tiles // split + 1  # the piece's second tile
+        keys += [64 * t, 64 * t + 4]
+    q, k, v = _dominant_keys(Sk, keys, 126.5, 0.25)
+    want = oracle.attention(q.double(), k.double(), v.double(), 128 ** -0.5)
+    out = torch.full(q.shape, float("nan"), dtype=BF, device=device)
+    pkg.make_attention(split_last_round=True)(q.to(device), k.to(device), v.to(device), 128 ** -0.5, out)
+    torch.cuda.synchronize()
+    mx, rel = attention_error(out.cpu(), want)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
 # ------------------------------------------------------------ key split of the last round
 
 WS_SLOT_BYTES = (256 * 128 + 256 * 2) * 4  # per piece: O of its 256 queries + (m, l) per query
