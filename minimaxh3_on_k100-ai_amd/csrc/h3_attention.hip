@@ -48,6 +48,7 @@
 #include <type_traits>
 
 #include "h3_common.hpp"
+#include "h3_internal.hpp"
 
 namespace h3 {
 namespace {
@@ -958,6 +959,27 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a) {
 }
 
 }  // namespace
+
+// CUs of a device, looked up once per device.
+constexpr int kMaxDevices = 64;
+std::atomic<int> cu_count[kMaxDevices];
+
+int device_cus(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return 0;
+    int n = cu_count[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cu_count[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+int stream_device_cus(hipStream_t stream) {
+    int dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return 0;
+    return device_cus(dev);
+}
+
 }  // namespace h3
 
 using namespace h3;
@@ -1011,19 +1033,6 @@ SplitPlan plan_split(int64_t units, int64_t tiles, int n_cu) {
     return plan;
 }
 
-// CUs of a device, looked up once per device.
-constexpr int kMaxDevices = 64;
-std::atomic<int> cu_count[kMaxDevices];
-
-int device_cus(int dev) {
-    if (dev < 0 || dev >= kMaxDevices) return 0;
-    int n = cu_count[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        cu_count[dev].store(n, std::memory_order_relaxed);
-    }
-    return n;
-}
 
 // The launcher of both numerics: fp32_qk (logits scaled by c = scale log2 e in
 // fp32) and bf16_prescale (q rounded to bf16(c q) before the product).

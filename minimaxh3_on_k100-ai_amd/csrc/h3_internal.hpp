@@ -11,4 +11,11 @@ namespace h3 {
 int check_quantize_fp8_per_head(const NineToothedTensor &x, const NineToothedTensor &x8,
                                 const NineToothedTensor &descale);
 
+// The number of CUs of device `dev`, looked up once per device; 0 when the
+// lookup fails. (h3_attention.hip)
+int device_cus(int dev);
+
+// The same for the device `stream` belongs to. (h3_attention.hip)
+int stream_device_cus(hipStream_t stream);
+
 }  // namespace h3
