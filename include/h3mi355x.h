@@ -43,10 +43,18 @@ typedef struct NineToothedTensor {
 /* ---------------------------------------------------------------- attention */
 
 /* Non-causal full attention forward, O = softmax(Q K^T * scale) V.
- * q, o: [B, H, Sq, 128]; k, v: [B, H, Sk, 128]; any strides on B/H/S, unit
- * stride on the head dim, 16-byte aligned rows. Sq may differ from Sk (keys
- * past Sk are masked). scale: fp64 scalar. fp32 logits and softmax state, bf16
- * P for the P.V product, fp32 denominator.
+ * q, o: [B, H, Sq, 128]; k, v: [B, H, Sk, 128]; any strides (in elements, on
+ * every dimension) with 2-byte aligned elements. Views with unit head-dim
+ * stride and 16-byte aligned rows take the 16-byte tile path; any other view
+ * runs on an element-strided path with the same arithmetic. Sq may differ from
+ * Sk (keys past Sk are masked). scale: fp64 scalar. fp32 logits scaled by
+ * scale * log2(e), exp2, bf16 P for the P.V product. The softmax's
+ * stabilising maximum is each 256-query unit's first key tile's maximum, kept
+ * for the unit's later tiles (the unit is recomputed with the running
+ * maximum when anything overflows against it), and the denominator sums the
+ * same bf16-rounded P that weights V; the reference instead rescales at every
+ * new running maximum and sums P in fp32 before rounding (both orders stay
+ * within the operator's tolerance).
  * Replaces launch_h3_full_attention (tools/h3_attention.py:25-41,104-121;
  * called at patches/InfiniCore.patch:1421-1422 with the [B,S,H,D] -> [B,H,S,D]
  * stride swap of :1403-1411). */
@@ -77,8 +85,9 @@ NineToothedResult launch_h3_full_attention_ws(NineToothedStream stream, NineToot
 int64_t h3_full_attention_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk);
 
 /* The same operator built for head dim 72 (the Qwen vision tower's heads):
- * q, o: [B, H, Sq, 72]; k, v: [B, H, Sk, 72]; otherwise as
- * launch_h3_full_attention (fp32_qk numerics). Returns an error for any other
+ * q, o: [B, H, Sq, 72]; k, v: [B, H, Sk, 72]; views and masking as
+ * launch_h3_full_attention, fp32_qk numerics in the reference's own order
+ * (a running maximum with rescaling, fp32 denominator). Returns an error for any other
  * head dim, as launch_h3_full_attention does for a head dim other than 128.
  * Replaces launch_h3_vision_attention_72 (scripts/build_h3_attention.py:23-24,
  * tools/h3_attention.py:104-121 with head_dim=72; called at

@@ -90,7 +90,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct AttnArgs {
     const bf16_t *q, *k, *v;
     bf16_t *o;
-    int64_t qs[3], ks[3], vs[3], os[3];  // element strides of B, H, S (D is unit-stride)
+    int64_t qs[3], ks[3], vs[3], os[3];  // element strides of B, H, S
+    int64_t qd, kd, vd, od;               // element strides of D (1 except on the element-strided path)
     int B, H, Sq, Sk;
     int qblocks;                          // ceil(Sq / kBM)
     float c;                              // scale * log2(e)
@@ -146,16 +147,46 @@ __device__ __forceinline__ int tile_chunk(int row) {
 // masks those keys (their scores become -inf and their probabilities exactly
 // 0, which leaves the finite V rows without effect). DIM < 128: chunks past
 // DIM / 8 read the row's last chunk and are replaced by zeros.
-template <bool IS_K, int DIM>
+//
+// GEN (the element-strided path): the row's 8 elements are read one by one
+// with the head-dim stride d_stride, from any 2-byte aligned address.
+template <bool IS_K, int DIM, bool GEN = false>
 __device__ __forceinline__ void load_tile(const bf16_t *base, int64_t s_stride, int key0, int valid,
-                                          u32x4_t (&reg)[kLoadRows]) {
+                                          u32x4_t (&reg)[kLoadRows], int64_t d_stride = 1) {
 #pragma unroll
     for (int r = 0; r < kLoadRows; ++r) {
         const int row0 = tile_row(r);
         const int row = row0 < valid ? row0 : valid - 1;
         const int chunk = tile_chunk<IS_K>(row0), cc = chunk < DIM / 8 ? chunk : DIM / 8 - 1;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t *>(base + static_cast<int64_t>(key0 + row) * s_stride + cc * 8);
+        const bf16_t *src = base + static_cast<int64_t>(key0 + row) * s_stride;
+        u32x4_t v;
+        if constexpr (GEN) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+                w[e / 2] = static_cast<uint32_t>(src[(cc * 8 + e) * d_stride]) |
+                           (static_cast<uint32_t>(src[(cc * 8 + e + 1) * d_stride]) << 16);
+            v = u32x4_t{w[0], w[1], w[2], w[3]};
+        } else {
+            v = *reinterpret_cast<const u32x4_t *>(src + cc * 8);
+        }
         reg[r] = chunk < DIM / 8 ? v : u32x4_t{0u, 0u, 0u, 0u};
+    }
+}
+
+// Eight consecutive head-dim elements of a row from d0 on, as packed bf16:
+// a 16-byte load, or (GEN) element loads with the head-dim stride.
+template <bool GEN>
+__device__ __forceinline__ uint4 load_row8(const bf16_t *row, int d0, int64_t d_stride) {
+    if constexpr (GEN) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+            w[e / 2] = static_cast<uint32_t>(row[(d0 + e) * d_stride]) |
+                       (static_cast<uint32_t>(row[(d0 + e + 1) * d_stride]) << 16);
+        return make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        return *reinterpret_cast<const uint4 *>(row + d0);
     }
 }
 
@@ -319,8 +350,14 @@ __device__ __forceinline__ void attend_tile(const bf16_t *kt, const bf16_t *vt, 
 // below DIM are computed (72: 5 k-steps, dims 0..79, and 3 blocks, dims
 // 0..95; 22 MFMAs per tile and wave against 32), and only dims below DIM are
 // stored.
-template <bool NEG, bool BUF, int DIM>
+//
+// GEN: the element-strided path for views the 16-byte accesses cannot take (a
+// head-dim stride other than 1, or rows that are not 16-byte aligned): Q, K,
+// V and O move element by element with their strides (pointer path only);
+// the arithmetic is unchanged.
+template <bool NEG, bool BUF, int DIM, bool GEN = false>
 __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention_fwd_kernel(AttnArgs a) {
+    static_assert(!GEN || !BUF, "the element-strided path loads through registers");
     // Two buffers per operand as separate arrays: the loads into one buffer
     // then provably do not alias the reads of the other, so the compiler's
     // wait for the loads is not placed before those reads.
@@ -357,7 +394,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         for (int kk = 0; kk < kk_steps<DIM>(); ++kk) {
             // This lane's 8 dims; past the head dim, a valid chunk is read and zeroed.
             const int d0 = 16 * kk + 8 * half;
-            const uint4 u = *reinterpret_cast<const uint4 *>(qrow + (d0 < DIM ? d0 : DIM - 8));
+            const uint4 u = load_row8<GEN>(qrow, d0 < DIM ? d0 : DIM - 8, a.qd);
             qreg[qs][kk] = as_bf16x8(d0 < DIM ? u : make_uint4(0u, 0u, 0u, 0u));
         }
         if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
@@ -410,8 +447,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         dma_tile(vrs, vvoff, 0, lds_v0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
-        load_tile<true, DIM>(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg);
-        load_tile<false, DIM>(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg);
+        load_tile<true, DIM, GEN>(kbase, a.ks[2], 0, a.Sk < kBN ? a.Sk : kBN, kreg, a.kd);
+        load_tile<false, DIM, GEN>(vbase, a.vs[2], 0, a.Sk < kBN ? a.Sk : kBN, vreg, a.vd);
         store_tile(lds_k0, kreg);
         store_tile(lds_v0, vreg);
     }
@@ -445,8 +482,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
             // they need no branch either.
             const int n0 = has_next ? next0 : a.Sk - 1;
             const int nvalid = a.Sk - n0 < kBN ? a.Sk - n0 : kBN;
-            load_tile<true, DIM>(kbase, a.ks[2], n0, nvalid, kreg);
-            load_tile<false, DIM>(vbase, a.vs[2], n0, nvalid, vreg);
+            load_tile<true, DIM, GEN>(kbase, a.ks[2], n0, nvalid, kreg, a.kd);
+            load_tile<false, DIM, GEN>(vbase, a.vs[2], n0, nvalid, vreg, a.vd);
         }
         attend_tile<false, NEG, DIM>(kc, vc, kBN, qreg, acc, m_run, l_run, c_loop, kidx, half, vidx);
         if constexpr (BUF) {
@@ -486,7 +523,17 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
                 uint2 w;
                 w.x = pack2(acc[db][qs][4 * g + 0] * inv, acc[db][qs][4 * g + 1] * inv);
                 w.y = pack2(acc[db][qs][4 * g + 2] * inv, acc[db][qs][4 * g + 3] * inv);
-                if (32 * db + 8 * g + 4 * half < DIM) *reinterpret_cast<uint2 *>(orow + 32 * db + 8 * g + 4 * half) = w;
+                const int d0 = 32 * db + 8 * g + 4 * half;
+                if (d0 < DIM) {
+                    if constexpr (GEN) {
+                        orow[d0 * a.od] = static_cast<bf16_t>(w.x);
+                        orow[(d0 + 1) * a.od] = static_cast<bf16_t>(w.x >> 16);
+                        orow[(d0 + 2) * a.od] = static_cast<bf16_t>(w.y);
+                        orow[(d0 + 3) * a.od] = static_cast<bf16_t>(w.y >> 16);
+                    } else {
+                        *reinterpret_cast<uint2 *>(orow + d0) = w;
+                    }
+                }
             }
     }
 }
@@ -1058,7 +1105,13 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
     if (!same_shape(qv, ov) || !same_shape(kv, vv)) return kInvalid;
     if (qv.shape[0] != kv.shape[0] || qv.shape[1] != kv.shape[1] || qv.shape[3] != kv.shape[3]) return kInvalid;
     if (qv.shape[3] != dim) return kInvalid;
-    if (!rows_vec16(qv, 2) || !rows_vec16(kv, 2) || !rows_vec16(vv, 2) || !rows_vec16(ov, 2)) return kInvalid;
+    // Views the 16-byte accesses cannot take run on the element-strided path
+    // (the reference's launcher likewise dispatches such views to its generic
+    // stride variant, patches/ninetoothed.patch:131-169).
+    const bool gen = !rows_vec16(qv, 2) || !rows_vec16(kv, 2) || !rows_vec16(vv, 2) || !rows_vec16(ov, 2);
+    if ((reinterpret_cast<uintptr_t>(qv.data) | reinterpret_cast<uintptr_t>(kv.data) |
+         reinterpret_cast<uintptr_t>(vv.data) | reinterpret_cast<uintptr_t>(ov.data)) & 1)
+        return kInvalid;  // bf16 elements are 2-byte aligned
     if (qv.shape[0] == 0 || qv.shape[1] == 0 || qv.shape[2] == 0) return 0;
     if (kv.shape[2] == 0) return kInvalid;  // softmax over no keys is undefined
     if (qv.shape[2] > kMaxSeqLen || kv.shape[2] > kMaxSeqLen) return kInvalid;
@@ -1073,6 +1126,10 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
         a.vs[i] = vv.stride[i];
         a.os[i] = ov.stride[i];
     }
+    a.qd = qv.stride[3];
+    a.kd = kv.stride[3];
+    a.vd = vv.stride[3];
+    a.od = ov.stride[3];
     a.B = static_cast<int>(qv.shape[0]);
     a.H = static_cast<int>(qv.shape[1]);
     a.Sq = static_cast<int>(qv.shape[2]);
@@ -1091,7 +1148,7 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
     const int64_t k_ext = extent(a.ks[2]), v_ext = extent(a.vs[2]);
     const int64_t reach = (static_cast<int64_t>(a.Sk) + 2 * kBN) * 2 *
                           (a.ks[2] > a.vs[2] ? a.ks[2] : a.vs[2]);
-    const bool buf = k_ext > 0 && v_ext > 0 && reach < (int64_t{1} << 30);
+    const bool buf = !gen && k_ext > 0 && v_ext > 0 && reach < (int64_t{1} << 30);
     a.k_bytes = buf ? static_cast<int>(k_ext) : 0;
     a.v_bytes = buf ? static_cast<int>(v_ext) : 0;
     const unsigned g = static_cast<unsigned>(grid);
@@ -1131,10 +1188,13 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
             attention16_kernel<false, false><<<g, kThreadsWG, 0, st>>>(a);
         return launch_status();
     }
-#define H3_ATTN(N, B, D) \
-    if (neg == N && buf == B && dim == D) attention_fwd_kernel<N, B, D><<<g, kThreadsWG, 0, st>>>(a);
-    H3_ATTN(false, false, 128) H3_ATTN(true, false, 128)
-    H3_ATTN(false, true, 72) H3_ATTN(false, false, 72) H3_ATTN(true, true, 72) H3_ATTN(true, false, 72)
+#define H3_ATTN(N, B, D, G) \
+    if (neg == N && buf == B && dim == D && gen == G) attention_fwd_kernel<N, B, D, G><<<g, kThreadsWG, 0, st>>>(a);
+    H3_ATTN(false, false, 128, false) H3_ATTN(true, false, 128, false)
+    H3_ATTN(false, true, 72, false) H3_ATTN(false, false, 72, false) H3_ATTN(true, true, 72, false)
+    H3_ATTN(true, false, 72, false)
+    H3_ATTN(false, false, 128, true) H3_ATTN(true, false, 128, true) H3_ATTN(false, false, 72, true)
+    H3_ATTN(true, false, 72, true)
 #undef H3_ATTN
     return launch_status();
 }

@@ -1,8 +1,10 @@
 """Non-causal full attention forward on gfx950 MFMA.
 
 Drop-in for tools/h3_attention.py: `make_attention` takes the same keywords and
-returns kernel(q, k, v, scale, out) on [B, H, S, D] tensors (any strides on B,
-H and S, unit stride on D), with Sq free to differ from Sk. The tile keywords
+returns kernel(q, k, v, scale, out) on [B, H, S, D] tensors of any strides
+(views without a unit head-dim stride or with rows that are not 16-byte
+aligned run on an element-strided path, as the reference's generic stride
+variant does), with Sq free to differ from Sk. The tile keywords
 (block_m, block_n, num_warps, num_stages, backend_options) are accepted for
 signature compatibility; the gfx950 kernel uses its own tiles (256 queries x
 64 keys per step).

@@ -171,10 +171,12 @@ CASES = [
                                   t([1, 2, 8, 128])], "head count mismatch"),
     ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 9, 128]), t([1, 2, 8, 128]), scal(0.1),
                                   t([1, 2, 8, 128])], "k/v length mismatch"),
-    ("launch_h3_full_attention", [t([1, 2, 8, 128], [2048, 1024, 128, 2]), t([1, 2, 8, 128]),
-                                  t([1, 2, 8, 128]), scal(0.1), t([1, 2, 8, 128])], "non-unit head-dim stride"),
-    ("launch_h3_full_attention", [t([1, 2, 8, 128], data=ADDR + 2), t([1, 2, 8, 128]), t([1, 2, 8, 128]),
-                                  scal(0.1), t([1, 2, 8, 128])], "misaligned q"),
+    # Views with any strides and 2-byte aligned rows run (element-strided
+    # path); a bf16 element at an odd address does not.
+    ("launch_h3_full_attention", [t([1, 2, 8, 128], data=ADDR + 1), t([1, 2, 8, 128]), t([1, 2, 8, 128]),
+                                  scal(0.1), t([1, 2, 8, 128])], "odd address q"),
+    ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 8, 128]), t([1, 2, 8, 128]),
+                                  scal(0.1), t([1, 2, 8, 128], data=ADDR + 3)], "odd address o"),
     ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 0, 128]), t([1, 2, 0, 128]), scal(0.1),
                                   t([1, 2, 8, 128])], "no keys"),
     ("launch_h3_full_attention", [t([1, 2, 8, 128]), t([1, 2, 8, 128]), t([1, 2, 8, 128]), NULLSCALAR,
@@ -187,8 +189,8 @@ CASES = [
      "head dim 128 on the 72 launcher"),
     ("launch_h3_vision_attention_72", [t([1, 2, 8, 72]), t([1, 2, 9, 72]), t([1, 2, 8, 72]), scal(0.1),
                                        t([1, 2, 8, 72])], "vision k/v length mismatch"),
-    ("launch_h3_vision_attention_72", [t([1, 2, 8, 72], [1152, 576, 72, 2])] + [t([1, 2, 8, 72])] * 2
-     + [scal(0.1), t([1, 2, 8, 72])], "vision non-unit head-dim stride"),
+    ("launch_h3_vision_attention_72", [t([1, 2, 8, 72])] * 2 + [t([1, 2, 8, 72], data=ADDR + 1)]
+     + [scal(0.1), t([1, 2, 8, 72])], "vision odd address v"),
     ("launch_h3_vision_attention_72", [t([1, 2, 8, 72]), t([1, 2, 0, 72]), t([1, 2, 0, 72]), scal(0.1),
                                        t([1, 2, 8, 72])], "vision no keys"),
     # fp8 quantiser: x [B, H, S, 128] bf16, codes u8, descale [H] fp32; every

@@ -100,6 +100,98 @@ def test_attention_broadcast_keys_take_the_pointer_path(pkg, oracle, device):
     assert (out.cpu().float() - vrow.float()).abs().max().item() <= 2 ** -7 * vrow.float().abs().max().item()
 
 
+def _strided(x, device, case, gen):
+    """x [B, H, S, D] on `device` as the view `case` names, sentinels around:
+    "dstride2": every other element of a [.., 2D] buffer (head-dim stride 2);
+    "offset1": rows starting one element into their buffer (2-byte aligned,
+    not 16); "odd_rows": an S stride of D + 3 elements; "dense": the
+    contiguous view. Returns (view, its buffer or None)."""
+    B, H, S, D = x.shape
+    if case == "dense":
+        return x.to(device).contiguous(), None
+    if case == "dstride2":
+        buf = torch.randn(B, H, S, 2 * D, generator=gen).to(BF)
+        buf[..., ::2] = x
+        return buf.to(device)[..., ::2], buf.to(device)
+    if case == "offset1":
+        buf = torch.randn(B, H, S, D + 1, generator=gen).to(BF)
+        buf[..., 1:] = x
+        return buf.to(device)[..., 1:], buf.to(device)
+    if case == "odd_rows":
+        buf = torch.randn(B, H, S, D + 3, generator=gen).to(BF)
+        buf[..., :D] = x
+        return buf.to(device)[..., :D], buf.to(device)
+    raise ValueError(case)
+
+
+@pytest.mark.parametrize("dim", [128, 72])
+@pytest.mark.parametrize("cases", [
+    ("dstride2", "dense", "dense", "dense"),
+    ("dense", "offset1", "dstride2", "dense"),
+    ("offset1", "odd_rows", "odd_rows", "dstride2"),
+    ("dense", "dense", "dense", "offset1"),
+])
+def test_attention_element_strided_views(pkg, oracle, device, dim, cases):
+    """Views the 16-byte accesses cannot take -- a head-dim stride other than
+    1, rows that are 2- but not 16-byte aligned, S strides
+    that are not multiples of 8 -- run on the element-strided path, as the
+    reference's generic stride variant does (patches/ninetoothed.patch:131-169):
+    within the operator's bar of the fp64 oracle, Sq not a multiple of 256 and
+    Sk not of 64, and the out buffer's elements outside the view untouched."""
+    gen = torch.Generator("cpu").manual_seed(dim + len("".join(cases)))
+    B, H, Sq, Sk = 2, 2, 300, 129
+    q = torch.randn(B, H, Sq, dim, generator=gen).to(BF)
+    k = torch.randn(B, H, Sk, dim, generator=gen).to(BF)
+    v = torch.randn(B, H, Sk, dim, generator=gen).to(BF)
+    qd, _ = _strided(q, device, cases[0], gen)
+    kd, _ = _strided(k, device, cases[1], gen)
+    vd, _ = _strided(v, device, cases[2], gen)
+    out, out_buf = _strided(torch.full((B, H, Sq, dim), float("nan")).to(BF), device, cases[3], gen)
+    before = out_buf.clone() if out_buf is not None else None
+    scale = dim ** -0.5
+    print(f"strided attention dim={dim} cases={cases}", flush=True)
+    pkg.make_attention(head_dim=dim)(qd, kd, vd, scale, out)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q, k, v, scale)
+    mx, rel = attention_error(out.cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+    if out_buf is not None:
+        inside = torch.zeros(out_buf.shape, dtype=torch.bool, device=device)
+        if cases[3] == "dstride2":
+            inside[..., ::2] = True
+        elif cases[3] == "offset1":
+            inside[..., 1:] = True
+        else:
+            inside[..., :dim] = True
+        assert torch.equal(out_buf[~inside].view(torch.int16), before[~inside].view(torch.int16)), "wrote outside the view"
+
+
+def test_attention_negative_head_dim_stride_through_the_abi(pkg, oracle, device):
+    """A view torch cannot express, handed to launch_h3_full_attention as the
+    C ABI allows: q, k, v and o with head-dim stride -1 (data points at each
+    row's last element). Same bar against the fp64 oracle of the reversed
+    rows."""
+    L = pkg._lib
+    gen = torch.Generator("cpu").manual_seed(77)
+    B, H, Sq, Sk, D = 1, 2, 200, 100, 128
+    q, k, v = (torch.randn(B, H, s, D, generator=gen).to(BF) for s in (Sq, Sk, Sk))
+    stores = [t.flip(-1).contiguous().to(device) for t in (q, k, v)]
+    o_store = torch.full((B, H, Sq, D), float("nan"), dtype=BF, device=device)
+
+    def rev(t):  # element (b, h, s, d) of the view is t_store[b, h, s, D - 1 - d]
+        sb, sh, ss, _ = t.stride()
+        return L.raw_tensor(t.data_ptr() + 2 * (D - 1), list(t.shape), [sb, sh, ss, -1])
+
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rc = L.call("launch_h3_full_attention", stream, rev(stores[0]), rev(stores[1]), rev(stores[2]),
+                L.scalar(128 ** -0.5), rev(o_store))
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    ref = oracle.attention(q, k, v, 128 ** -0.5)
+    mx, rel = attention_error(o_store.flip(-1).cpu(), ref)
+    assert mx <= MAX_ABS and rel <= REL_RMS, (mx, rel)
+
+
 @pytest.mark.parametrize("scale", [128 ** -0.5, -0.07])
 def test_attention_bf16_prescale(pkg, oracle, device, scale):
     """numerics="bf16_prescale" (tools/h3_attention.py:87-101) against its own
