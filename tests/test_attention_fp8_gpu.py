@@ -170,6 +170,20 @@ def _run(pkg, device, q, k, v, scale, mode):
     return out
 
 
+# Kernel-to-emulation distance bars, about twice the largest measured on an
+# MI355X over this file's cases (relative RMS: fp8 1.5e-3, fp8pv 3.4e-4, fp8x2
+# 2.3e-3; max abs under 1e-2 for all). The kernel departs from the emulation
+# only in fp32 summation order inside the MFMAs and in exp2's last bit, which
+# can move a 448 P across an e4m3 rounding boundary.
+EMU_REL = {"fp8": 3e-3, "fp8pv": 8e-4, "fp8x2": 5e-3}
+EMU_MAX = 2e-2
+
+
+def _emu_check(mode, q, k, scale, mx, rel):
+    print(f"EMU {mode} {tuple(q.shape)} {tuple(k.shape)} scale {scale:+.3f}: rel {rel:.3e} max {mx:.3e}", flush=True)
+    assert rel <= EMU_REL[mode] and mx <= EMU_MAX, (mode, mx, rel)
+
+
 def _emulated(oracle, q, k, v, scale, mode):
     v8, vd = oracle.quantize_fp8_per_head(v)
     if mode == "fp8":
@@ -191,7 +205,7 @@ def test_fp8_attention_matches_emulation(pkg, oracle, device, mode, S, H):
     out = _run(pkg, device, q, k, v, scale, mode)
     emu = _emulated(oracle, q, k, v, scale, mode)
     mx, rel = attention_error(out.cpu(), emu)
-    assert rel <= 1.5e-2 and mx <= 0.05, (mode, mx, rel)
+    _emu_check(mode, q, k, scale, mx, rel)
     if mode in ("fp8pv", "fp8x2"):  # the fp8 configuration's bar; the one-term all-fp8 recipe misses it
         ref = oracle.attention(q, k, v, scale)
         _, rel_ref = attention_error(out.cpu(), ref)
@@ -210,7 +224,7 @@ def test_fp8_attention_negative_scale(pkg, oracle, device, mode, S, H):
     out = _run(pkg, device, q, k, v, scale, mode)
     emu = _emulated(oracle, q, k, v, scale, mode)
     mx, rel = attention_error(out.cpu(), emu)
-    assert rel <= 1.5e-2 and mx <= 0.05, (mode, mx, rel)
+    _emu_check(mode, q, k, scale, mx, rel)
     pos = _run(pkg, device, q, k, v, -scale, mode)
     _, rel_pos = attention_error(out.cpu(), pos.cpu())
     assert rel_pos > 0.2, rel_pos
@@ -253,7 +267,7 @@ def test_fp8_attention_ragged_batched(pkg, oracle, device, mode, B, H, Sq, Sk):
     out = _run(pkg, device, q, k, v, scale, mode)
     emu = _emulated(oracle, q, k, v, scale, mode)
     mx, rel = attention_error(out.cpu(), emu)
-    assert rel <= 1.5e-2 and mx <= 0.05, (mode, mx, rel)
+    _emu_check(mode, q, k, scale, mx, rel)
 
 
 @pytest.mark.parametrize("mode", ["fp8x2", "fp8pv", "fp8"])

@@ -10,7 +10,7 @@ oracle's outputs for them.
   bitwise for the pointwise ops and the quantiser, the RoPE table within 1
   bf16 ulp (device cosf/sinf vs the CPU's); attention
   within the bf16 tolerance (max abs <= 2e-2, relative RMS <= 1e-2); the fp8
-  P.V variant within relative RMS 1.5e-2 of its emulation.
+  P.V variant within relative RMS 1e-3 of its emulation.
 """
 from __future__ import annotations
 
@@ -175,4 +175,5 @@ def test_kernels_match_golden_attention(g, pkg, device):
     pkg.make_attention_fp8pv()(q, k, v8, vd, scale, out8)
     torch.cuda.synchronize()
     _, rel8 = attention_error(out8.cpu(), bf(g["fp8pv_out"]))
-    assert rel8 <= 1.5e-2, rel8
+    print(f"EMU golden fp8pv: rel {rel8:.3e}", flush=True)
+    assert rel8 <= 1e-3, rel8  # the fp8pv kernel-to-emulation distance measures at most 3.4e-4

@@ -270,7 +270,7 @@ def test_qkv_pack_fp8x2_feeds_fp8x2_attention(pkg, oracle, device):
     """The fp8 configuration's pipeline on one rank: the two-term pack (q, k
     codes and V's amax slots), V^T quantised from the slots, the two-term
     attention; within relative RMS 5e-2 of fp32 attention on the packed bf16
-    q, k, v, and within 1.5e-2 of the oracle's emulation of the same codes."""
+    q, k, v, and within 4e-3 of the oracle's emulation of the same codes."""
     T, P, Hs = 4096, 1, 4
     projected, wq, wk, cache, positions = _case(T, P, Hs, 5, device)
     q, k, v = pkg.qkv_by_rank(projected.to(device), P)
@@ -295,7 +295,8 @@ def test_qkv_pack_fp8x2_feeds_fp8x2_attention(pkg, oracle, device):
                                         kd.cpu(), vd.cpu(), scale,
                                         lo_terms=(bhsd(ql).cpu(), qd.cpu() / 16, bhsd(kl).cpu(), kd.cpu() / 16))
     rel_emu = float((out.cpu().double() - emu.double()).norm() / emu.double().norm())
-    assert rel_emu <= 1.5e-2, rel_emu
+    print(f"EMU pack pipeline: rel {rel_emu:.3e}", flush=True)
+    assert rel_emu <= 4e-3, rel_emu  # measured 1.7e-3 on an MI355X
 
 
 @pytest.mark.gpu
