@@ -44,6 +44,7 @@ import importlib
 import json
 import math
 import os
+import platform
 import statistics
 import sys
 import time
@@ -367,12 +368,47 @@ def bench_pointwise(pkg, device) -> dict:
     return results
 
 
+def cpu_host() -> dict:
+    """The host CPU the CPU figures run on: its model, the CPUs the OS reports
+    and the ones this process may run on, and torch's thread count (the
+    threads every CPU figure uses: the GPU box grants a job a share of its
+    CPUs and sets OMP_NUM_THREADS to it, which torch follows)."""
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "usable_cpus": usable,
+            "threads": torch.get_num_threads()}
+
+
+def median_time(fn, warmup: int = 3, runs: int = 5) -> float:
+    """Median seconds of `runs` calls after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
 def cpu_reference_path(device, pointwise: dict | None, attention_s8192: dict | None) -> None:
     """The reference's torch CPU path beside each measured op: the oracle's
     restatement of the torch compositions (order="torch", the literal eager
     sums; tools/bench_h3_ops.py:81-113,145-149,215,232-234,251-254) at the
-    configuration sizes, once each after a small warm-up, on this host's
-    threads; and the fp32 attention at S = 8192, H = 14. Adds "cpu_us" /
+    configuration sizes, the median of 5 runs after 3 warm-ups each, on this
+    host's threads; and the fp32 attention at S = 8192, H = 14 (the median of 3
+    runs after one warm-up). Adds "cpu_us" /
     "cpu_GB/s" (same algorithmic bytes as the GPU figure) to the pointwise
     entries and "cpu_TFLOP/s" to the S = 8192 line. Inputs are drawn on the
     GPU from a seeded generator and copied to the host (same shapes and
@@ -384,13 +420,8 @@ def cpu_reference_path(device, pointwise: dict | None, attention_s8192: dict | N
     def rnd(*shape, scale=1.0, offset=0.0):
         return (torch.randn(*shape, generator=gen, device=device) * scale + offset).to(bf).cpu()
 
-    def timed(fn) -> float:
-        t0 = time.perf_counter()
-        fn()
-        return time.perf_counter() - t0
-
+    timed = median_time
     threads = torch.get_num_threads()
-    h3_oracle.rms_modulate(rnd(1, 64, 7168), rnd(7168), 1e-6, rnd(1, 1, 7168), rnd(1, 1, 7168), order="torch")
 
     def note(name, seconds):
         if pointwise is None or name not in pointwise:
@@ -423,7 +454,8 @@ def cpu_reference_path(device, pointwise: dict | None, attention_s8192: dict | N
     if attention_s8192 is not None:
         S2, H = 8192, 14
         q, k, v = (rnd(1, H, S2, 128) for _ in range(3))
-        seconds = timed(lambda: h3_oracle.attention(q, k, v, 128 ** -0.5, dtype=torch.float32, chunk=2048))
+        seconds = median_time(lambda: h3_oracle.attention(q, k, v, 128 ** -0.5, dtype=torch.float32, chunk=2048),
+                              warmup=1, runs=3)
         attention_s8192["cpu_TFLOP/s"] = round(4.0 * H * S2 * S2 * 128 / seconds / 1e12, 4)
         attention_s8192["cpu_threads"] = threads
         log(f"  cpu attention S={S2}: {seconds:.2f} s, {attention_s8192['cpu_TFLOP/s']} TFLOP/s ({threads} threads)")
@@ -447,9 +479,11 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
         elapsed += time.perf_counter() - t_head
         flops += 4.0 * S * S * 128
         heads += 1
+    host = cpu_host()
     return {"value": round(flops / elapsed / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"{heads} of 14 heads of the S=73,984 D=128 attention, fp32 on the host CPU "
-                      f"(oracle softmax(q k^T s) v, 2048-query chunks), {elapsed:.1f} s"}
+                      f"(oracle softmax(q k^T s) v, 2048-query chunks), {elapsed:.1f} s",
+            "cpu_model": host["cpu_model"], "host_cpus": host["host_cpus"], "usable_cpus": host["usable_cpus"]}
 
 
 def mfma_peak_measured(pkg, device, headline_tflops: float | None) -> dict:
