@@ -99,3 +99,85 @@ def test_noalloc_pack_python_face(pkg, device):
                                            transposed=True)
     assert torch.equal(refd.cpu(), res[0][6])
     assert torch.equal(ref8.cpu().view(torch.uint8), res[0][5])
+
+
+_CAPTURE_SCRIPT = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import importlib
+import torch
+from test_qkv_pack import _case
+from test_zz_no_alloc import _v8_view, _pack_args
+
+pkg = importlib.import_module("minimaxh3_on_k100-ai_amd")
+L = pkg._lib
+device = torch.device("cuda:0")
+BF = torch.bfloat16
+T, Hs = 1000, 6
+projected, wq, wk, cache, positions = _case(T, 1, Hs, 13, device)
+projected = projected.to(device)
+q, k, v = pkg.qkv_by_rank(projected, 1)
+wq, wk, cache, positions = wq.to(device), wk.to(device), cache.to(device), positions.to(device)
+
+
+def buffers():
+    q8 = torch.zeros(T, 1, Hs, 128, dtype=torch.uint8, device=device)
+    return dict(q8=q8, k8=torch.zeros_like(q8), v_out=torch.zeros(T, 1, Hs, 128, dtype=BF, device=device),
+                qd=torch.zeros(Hs, device=device), kd=torch.zeros(Hs, device=device),
+                v8=_v8_view(T, Hs, device, 0), vd=torch.zeros(Hs, device=device))
+
+
+def args(b):
+    return _pack_args(L, q, k, v, wq, wk, cache, positions, b["q8"], b["k8"], b["v_out"], b["qd"], b["kd"])
+
+
+graph_b, eager_b = buffers(), buffers()
+side = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+torch.cuda.synchronize()
+print("capturing the first allocation-free call of this process", flush=True)
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        rc = L.call("launch_h3_qkv_norm_rope_pack_fp8_noalloc", side.cuda_stream, *args(graph_b),
+                    L.tensor(graph_b["v8"]), L.tensor(graph_b["vd"]))
+assert rc == 0, rc
+torch.cuda.synchronize()
+gen = torch.Generator(device=device).manual_seed(3)
+stream = torch.cuda.current_stream(device).cuda_stream
+for replay in range(3):
+    projected.copy_((torch.randn(projected.shape, generator=gen, device=device) * (1 + replay)).to(BF))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    slots = torch.full((Hs, L.AMAX_SLOTS), float("nan"), device=device)
+    assert L.call("launch_h3_qkv_norm_rope_pack_fp8_vamax", stream, *args(eager_b), L.tensor(slots)) == 0
+    v_rows = eager_b["v_out"][:, 0].unsqueeze(0).transpose(1, 2)
+    assert L.call("launch_h3_quantize_fp8_per_head_slots", stream, L.tensor(v_rows), L.tensor(slots),
+                  L.tensor(eager_b["v8"]), L.tensor(eager_b["vd"])) == 0
+    torch.cuda.synchronize()
+    for name in graph_b:
+        a, b = graph_b[name], eager_b[name]
+        same = torch.equal(a.view(torch.int16), b.view(torch.int16)) if a.dtype == BF else torch.equal(a, b)
+        assert same, (replay, name)
+    print(f"replay {replay} bitwise", flush=True)
+print("CAPTURE_OK", flush=True)
+'''
+
+
+@pytest.mark.gpu
+def test_noalloc_pack_first_call_inside_graph_capture(device):
+    """In a fresh process (so the device's slot address is not yet looked up),
+    the first call of launch_h3_qkv_norm_rope_pack_fp8_noalloc is made inside
+    a HIP graph capture; the graph is replayed three times, the projection
+    rewritten by eager work before each replay, and every output of every
+    replay equals the two-call sequence (caller's slots) run eagerly on the
+    same inputs, bitwise."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    proc = subprocess.run([sys.executable, "-u", "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True,
+                          timeout=240)
+    print(proc.stdout[-2000:], proc.stderr[-2000:])
+    assert proc.returncode == 0 and "CAPTURE_OK" in proc.stdout, proc.returncode
