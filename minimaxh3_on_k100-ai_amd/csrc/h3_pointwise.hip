@@ -1567,12 +1567,32 @@ struct QkvArgs {
 constexpr float kQkFp8BoundPerWeight = 11.667261889577f;  // fp32(sqrt(128) * 1.03125)
 constexpr float kE4M3Max = 448.0f;
 
-// Eight fp32 values (already bf16) as e4m3fn codes: e4m3(sat((f * pre) *
-// inv)), the scale of e4m3_code_scale.
-__device__ __forceinline__ uint2 e4m3x8(const float f[8], float pre, float inv) {
-    float y[8];
+// The scaled values of eight outputs (already bf16): y = sat((f * pre) * inv),
+// the scale of e4m3_code_scale. pre is 1 except for a bound below about
+// 1.3e-36, and f * 1 = f exactly, so a launch with pre = 1 (every block of it
+// the same) skips that product. sat() is applied only when some |y| exceeds
+// 448 (a cos/sin table that is not a rotation can exceed the weight bound);
+// otherwise it changes nothing: values within +-448 are kept, and a NaN --
+// which fmaxf passes over -- stays NaN either way.
+__device__ __forceinline__ void e4m3_scaled8(const float f[8], float pre, float inv, float y[8]) {
+    if (pre == 1.0f) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = sat_e4m3((f[e] * pre) * inv);
+        for (int e = 0; e < 8; ++e) y[e] = f[e] * inv;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (f[e] * pre) * inv;
+    }
+    float m = fabsf(y[0]);
+#pragma unroll
+    for (int e = 1; e < 8; ++e) m = fmaxf(m, fabsf(y[e]));
+    if (m > 448.0f) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = sat_e4m3(y[e]);
+    }
+}
+
+// Eight scaled values (e4m3_scaled8) as e4m3fn codes.
+__device__ __forceinline__ uint2 e4m3x8(const float y[8]) {
     int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], lo, true);
     int hi = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
@@ -1580,11 +1600,12 @@ __device__ __forceinline__ uint2 e4m3x8(const float f[8], float pre, float inv) 
     return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
 }
 
-// The lo term of the two-term split of eight values: with y = sat((f * pre)
-// * inv) and hi = e4m3(y) (the codes of e4m3x8), e4m3(sat(16 (y - hi))); y -
-// hi is exact in fp32 and |16 (y - hi)| <= 256.
+// The lo term of the two-term split of eight scaled values y with codes hi =
+// e4m3x8(y): e4m3(16 (y - hi)). y - hi is exact in fp32 (hi is y rounded to 4
+// significant bits, or 0) and |16 (y - hi)| <= 256, so the saturation of the
+// quantiser's formula, e4m3(sat(16 (y - hi))), never acts and is left out.
 constexpr float kLoTermShift = 16.0f;
-__device__ __forceinline__ uint2 e4m3x8_lo(const float f[8], float pre, float inv, uint2 hi) {
+__device__ __forceinline__ uint2 e4m3x8_lo(const float y[8], uint2 hi) {
     float r[8];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -1593,10 +1614,7 @@ __device__ __forceinline__ uint2 e4m3x8_lo(const float f[8], float pre, float in
         const f32x2_t h23 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
         const float h[4] = {h01[0], h01[1], h23[0], h23[1]};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float y = sat_e4m3((f[4 * half + e] * pre) * inv);
-            r[4 * half + e] = sat_e4m3((y - h[e]) * kLoTermShift);
-        }
+        for (int e = 0; e < 4; ++e) r[4 * half + e] = (y[4 * half + e] - h[e]) * kLoTermShift;
     }
     int lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], lo, true);
@@ -1730,9 +1748,11 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
             if constexpr (FP8) {
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) rbf2(f[e], f[e + 1]);  // the bf16 output, then its codes
-                const uint2 codes = e4m3x8(f, pre, inv);
+                float y[8];
+                e4m3_scaled8(f, pre, inv, y);
+                const uint2 codes = e4m3x8(y);
                 uint2 lo_codes = {0u, 0u};
-                if constexpr (TWO) lo_codes = e4m3x8_lo(f, pre, inv, codes);
+                if constexpr (TWO) lo_codes = e4m3x8_lo(y, codes);
                 if (bt.ok[r]) {
 #pragma unroll
                     for (int term = 0; term < (TWO ? 2 : 1); ++term) {
