@@ -1554,6 +1554,7 @@ struct QkvArgs {
     float *q_descale, *k_descale;  // FP8: fp32 [P * Hs] each
     uint32_t *v_amax;              // VAMAX: [P * Hs, H3_AMAX_SLOTS] |v| maxima as fp32 bits
     char *q_out_lo, *k_out_lo;     // TWO: the lo codes, with q_out's / k_out's strides
+    bool v_pinned;                 // VAMAX: v blocks pinned to heads, at most H3_AMAX_SLOTS per head
 };
 
 // The fp8 epilogue's scale. An RMSNorm'd 128-vector n has sum(n^2) = 128, so
@@ -1658,6 +1659,93 @@ __global__ __launch_bounds__(kThreads) void qkv_pack_kernel(QkvArgs a) {
     const int lane = threadIdx.x & 15;
     const uint32_t group = threadIdx.x >> 4;
     const HeadRows in = pick3(kind, a.q, a.k, a.v), out = pick3(kind, a.q_out, a.k_out, a.v_out);
+    if constexpr (VAMAX) {
+        // V blocks pinned to heads (v_pinned: at least one v block per head):
+        // v block j copies the rows of head hp = j % (P Hs) only, the head's
+        // 16-row batches grid-strided over its n blocks (n <= H3_AMAX_SLOTS),
+        // so every lane keeps one running maximum of |v| in a register. The block folds it once at the end and stores it, as the
+        // k-th block of its head (k = j / (P Hs) < n), into slot k of the head,
+        // and zeros into slots k + n, k + 2n, ...: every slot of every head
+        // has exactly one writer, so the slots need no clearing and no atomics.
+        // The pinned blocks of all heads run together, so the reads still
+        // cover whole token rows at any moment.
+        const uint32_t heads = static_cast<uint32_t>(a.P * a.Hs);
+        if (kind == 2 && a.v_pinned) {
+            const uint32_t hp = tile0 % heads, first = tile0 / heads;
+            // The head's v blocks: those of index j = hp + k (P Hs), at most
+            // H3_AMAX_SLOTS of them (the others have no rows).
+            const uint32_t all = (tiles - hp + heads - 1) / heads;
+            const uint32_t step = all < H3_AMAX_SLOTS ? all : H3_AMAX_SLOTS;
+            if (first >= step) return;
+            const uint32_t T = static_cast<uint32_t>(a.rows / heads);
+            const uint32_t pp = hp / static_cast<uint32_t>(a.Hs), hh = hp - pp * static_cast<uint32_t>(a.Hs);
+            constexpr uint32_t kBatch = kGroups * R;
+            const uint32_t nb = (T + kBatch - 1) / kBatch;
+            struct VBatch {
+                bool ok[R];
+                int64_t out_off[R];
+                U4 xv[R];
+            };
+            // A row past the head's end re-reads its last token (the head's own
+            // values, so the maximum stays exact) and is not stored.
+            auto vload = [&](uint32_t i, VBatch &bt) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t t = i * kBatch + group + r * kGroups;
+                    bt.ok[r] = t < T;
+                    const uint32_t tc = t < T ? t : T - 1;
+                    bt.out_off[r] = head_offset<OFF32>(out, tc, pp, hh);
+                    bt.xv[r] = load_head<VEC>(in, head_offset<OFF32>(in, tc, pp, hh), lane);
+                }
+            };
+            uint32_t vm = 0;
+            auto vfinish = [&](VBatch &bt) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (bt.ok[r])
+                        store_group<VEC, true>(reinterpret_cast<bf16_t *>(out.p) + bt.out_off[r], out.s3, lane * 8,
+                                               128, bt.xv[r]);
+                    const uint32_t w[4] = {bt.xv[r].x, bt.xv[r].y, bt.xv[r].z, bt.xv[r].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t lo = (w[e] << 16) & 0x7fffffffu, hi = w[e] & 0x7fff0000u;
+                        vm = lo > vm ? lo : vm;
+                        vm = hi > vm ? hi : vm;
+                    }
+                }
+            };
+            if (first < nb) {
+                VBatch A, B;
+                uint32_t i = first;
+                vload(i, A);
+                while (true) {
+                    vload(i + step < nb ? i + step : i, B);
+                    vfinish(A);
+                    i += step;
+                    if (i >= nb) break;
+                    vload(i + step < nb ? i + step : i, A);
+                    vfinish(B);
+                    i += step;
+                    if (i >= nb) break;
+                }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const uint32_t o = __shfl_xor(vm, off, 64);
+                vm = o > vm ? o : vm;
+            }
+            __shared__ uint32_t wave_vm[kThreads / 64];
+            if ((threadIdx.x & 63) == 0) wave_vm[threadIdx.x >> 6] = vm;
+            __syncthreads();
+            uint32_t m = wave_vm[0];
+#pragma unroll
+            for (int w2 = 1; w2 < kThreads / 64; ++w2) m = wave_vm[w2] > m ? wave_vm[w2] : m;
+            uint32_t *slots = a.v_amax + static_cast<uint64_t>(hp) * H3_AMAX_SLOTS;
+            for (uint32_t j = first + threadIdx.x * step; j < H3_AMAX_SLOTS; j += kThreads * step)
+                slots[j] = j == first ? m : 0u;
+            return;
+        }
+    }
     RopeArgs ta{};
     ta.cos = a.cos;
     ta.sin = a.sin;
@@ -1905,8 +1993,15 @@ int launch_qkv_pack(hipStream_t stream, const View<4> *in, const View<4> *out, c
     }
     if (rows >= (int64_t{1} << 31) - kThreads * 4) return kInvalid;
     if (check_only) return 0;
-    if (vamax) {  // the slots start at 0 (an empty V has amax 0)
-        const int64_t n = a.P * a.Hs * H3_AMAX_SLOTS;
+    // kQkvBlocks blocks per tensor at most, one batch of kThreads / 16 rows each
+    // per turn.
+    constexpr int64_t kBatch = kThreads / 16 * kQkvRows;
+    const int64_t batches = (rows + kBatch - 1) / kBatch;
+    const int64_t tiles = batches < kQkvBlocks ? batches : kQkvBlocks;
+    const int64_t heads = a.P * a.Hs;
+    a.v_pinned = vamax && heads > 0 && tiles >= heads;
+    if (vamax && !a.v_pinned) {  // the slots start at 0 (an empty V has amax 0)
+        const int64_t n = heads * H3_AMAX_SLOTS;
         if (n > 0) clear_words_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(a.v_amax, n);
     }
     if (rows == 0) return vamax ? launch_status() : 0;
@@ -1915,11 +2010,7 @@ int launch_qkv_pack(hipStream_t stream, const View<4> *in, const View<4> *out, c
     bool off32 = offsets_fit_int32(cos) && offsets_fit_int32(sin) && offsets_fit_int32(pos) &&
                  a.P * a.Hs < (int64_t{1} << 24);
     for (int i = 0; i < 3; ++i) off32 = off32 && offsets_fit_int32(in[i]) && offsets_fit_int32(out[i]);
-    // kQkvBlocks blocks per tensor at most, one batch of kThreads / 16 rows each
-    // per turn.
-    constexpr int64_t kBatch = kThreads / 16 * kQkvRows;
-    const int64_t batches = (rows + kBatch - 1) / kBatch;
-    const unsigned g = static_cast<unsigned>(3 * (batches < kQkvBlocks ? batches : kQkvBlocks));
+    const unsigned g = static_cast<unsigned>(3 * tiles);
 #define H3_QKV(V, O, F, A) \
     if (vec == V && off32 == O && fp8 == F && vamax == A && !two) \
         qkv_pack_kernel<V, kQkvRows, O, F, A><<<g, kThreads, 0, stream>>>(a);
