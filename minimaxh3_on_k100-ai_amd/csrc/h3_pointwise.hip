@@ -1605,17 +1605,21 @@ __device__ __forceinline__ uint2 e4m3x8(const float y[8]) {
 // e4m3x8(y): e4m3(16 (y - hi)). y - hi is exact in fp32 (hi is y rounded to 4
 // significant bits, or 0) and |16 (y - hi)| <= 256, so the saturation of the
 // quantiser's formula, e4m3(sat(16 (y - hi))), never acts and is left out.
+// 16 hi comes straight from the scaled conversion (v_cvt_scalef32_pk_f32_fp8
+// with scale 16 equals the plain conversion times 16 for all 65,536 code
+// pairs, measured on the hardware), and 16 (y - hi) = fma(y, 16, -16 hi): the
+// exact value is representable, so the one rounding of the fma leaves it.
 constexpr float kLoTermShift = 16.0f;
 __device__ __forceinline__ uint2 e4m3x8_lo(const float y[8], uint2 hi) {
     float r[8];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         const int w = static_cast<int>(half == 0 ? hi.x : hi.y);
-        const f32x2_t h01 = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-        const f32x2_t h23 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-        const float h[4] = {h01[0], h01[1], h23[0], h23[1]};
+        const f32x2_t h01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, kLoTermShift, false);
+        const f32x2_t h23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, kLoTermShift, true);
+        const float h16[4] = {h01[0], h01[1], h23[0], h23[1]};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[4 * half + e] = (y[4 * half + e] - h[e]) * kLoTermShift;
+        for (int e = 0; e < 4; ++e) r[4 * half + e] = __builtin_fmaf(y[4 * half + e], kLoTermShift, -h16[e]);
     }
     int lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], lo, true);
