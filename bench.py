@@ -165,6 +165,37 @@ def time_launches(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def graph_kernel_time(calls, replays: int = 10) -> float | None:
+    """Milliseconds of device kernel time per call of `calls` (the library's
+    kernels only), from torch's profiler over `replays` replays of one HIP
+    graph of them: the kernels' own durations, without the gaps between
+    graph nodes that time_graph's per-launch figure includes. None if the
+    profiler records none of them."""
+    from torch.profiler import ProfilerActivity, profile
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for _ in range(replays):
+            graph.replay()
+        torch.cuda.synchronize()
+    total_us = 0.0
+    found = 0
+    for e in prof.events():
+        if "h3::" in e.name:
+            total_us += getattr(e, "device_time_total", None) or e.cuda_time_total
+            found += 1
+    if found == 0:
+        return None
+    return total_us / 1e3 / (replays * len(calls))
+
+
 def time_graph(calls, repeats: int = 20, rounds: int = 5) -> float:
     """Milliseconds per launch of `calls` (a list of zero-argument launches)
     captured back to back in one HIP graph: the median over `rounds` rounds of
@@ -210,25 +241,35 @@ def pattern_ceilings(pkg, device, read_bytes: int, n_in: int, n_out: int, row_by
     total = read_bytes * (n_in + n_out)
     out = {}
 
-    def entry(ms):
+    def entry(calls):
+        ms = time_graph(calls)
         gbs = total / (ms * 1e-3) / 1e9
-        return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        e = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        kms = graph_kernel_time(calls)
+        if kms is not None:
+            e["kernel_us"] = round(kms * 1e3, 2)
+            e["kernel_frac"] = round(total / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        return e
 
-    out["stream"] = entry(time_graph([lambda i=i, o=o: cal.stream(i[0], o[0], *(i[1:] + o[1:2] if n_in > 1 else ()))
-                                      for i, o in sets]))
+    out["stream"] = entry([lambda i=i, o=o: cal.stream(i[0], o[0], *(i[1:] + o[1:2] if n_in > 1 else ()))
+                           for i, o in sets])
     if row_bytes:
-        out["row_copy"] = entry(time_graph([lambda i=i, o=o: cal.row_copy(
-            i[0], o[0], row_bytes, *(i[1:] + o[1:2] if n_in > 1 else ())) for i, o in sets]))
+        out["row_copy"] = entry([lambda i=i, o=o: cal.row_copy(
+            i[0], o[0], row_bytes, *(i[1:] + o[1:2] if n_in > 1 else ())) for i, o in sets])
     del sets
     return out
 
 
 def bench_pointwise(pkg, device) -> dict:
     """GB/s per op; bytes = compulsory bf16 reads + writes (broadcast vectors
-    counted once). Beside each configuration op, `ceiling`: the same bytes
-    moved by a plain stream and (for the row-complete RMS family) by whole-row
-    copies, timed here, and `frac_of_ceiling`, the op's time against the best
-    of them."""
+    counted once). `us` / `frac`: per launch of a captured HIP graph of
+    back-to-back launches (the gaps between graph nodes included);
+    `kernel_us` / `kernel_frac`: the kernels' own device durations in the same
+    graph, from torch's profiler (the figure a kernel trace gives). Beside each
+    configuration op, `ceiling`: the same bytes moved by a plain stream and
+    (for the row-complete RMS family) by whole-row copies, timed the same two
+    ways, and `frac_of_ceiling` / `kernel_frac_of_ceiling`, the op's time
+    against the best of them."""
     results = {}
     gen = torch.Generator(device=device).manual_seed(0)
     bf = torch.bfloat16
@@ -236,20 +277,36 @@ def bench_pointwise(pkg, device) -> dict:
     def rnd(*shape, scale=1.0):
         return (torch.randn(*shape, generator=gen, device=device) * scale).to(bf)
 
+    last_calls: list = []
+
+    def timed(calls):
+        last_calls[:] = calls
+        return time_graph(calls)
+
     def record(name, ms, nbytes, shape):
         gbs = nbytes / (ms * 1e-3) / 1e9
         results[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                          "bytes": nbytes, "shape": shape}
-        log(f"  {name:34s} {ms * 1e3:8.2f} us  {gbs:8.1f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+        kms = graph_kernel_time(last_calls)
+        extra = ""
+        if kms is not None:
+            kgbs = nbytes / (kms * 1e-3) / 1e9
+            results[name].update({"kernel_us": round(kms * 1e3, 2), "kernel_GB/s": round(kgbs, 1),
+                                  "kernel_frac": round(kgbs / HBM_PEAK_GBS, 4)})
+            extra = f"; kernel alone {kms * 1e3:.2f} us ({kgbs / HBM_PEAK_GBS:.1%})"
+        log(f"  {name:34s} {ms * 1e3:8.2f} us  {gbs:8.1f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of HBM peak){extra}")
 
     def ceiling(name, read_bytes, n_in, n_out, row_bytes):
         entry = results[name]
         entry["ceiling"] = pattern_ceilings(pkg, device, read_bytes, n_in, n_out, row_bytes)
         best = min(c["us"] for c in entry["ceiling"].values())
         entry["frac_of_ceiling"] = round(best / entry["us"], 4)
-        log(f"  {'':34s} same bytes: " + ", ".join(f"{k} {c['us']:.2f} us ({c['frac']:.1%})"
-                                                    for k, c in entry["ceiling"].items())
-            + f"; op at {entry['frac_of_ceiling']:.1%} of the best")
+        kbest = [c["kernel_us"] for c in entry["ceiling"].values() if "kernel_us" in c]
+        if kbest and "kernel_us" in entry:
+            entry["kernel_frac_of_ceiling"] = round(min(kbest) / entry["kernel_us"], 4)
+        log(f"  {'':34s} same bytes: " + ", ".join(
+            f"{k} {c['us']:.2f} us ({c['frac']:.1%}; kernel alone {c.get('kernel_us', float('nan')):.2f} us)"
+            for k, c in entry["ceiling"].items()) + f"; op at {entry['frac_of_ceiling']:.1%} of the best")
 
     # q/k RMSNorm + RoPE, [1, 8192, 14, 128] per tensor, both layouts.
     T, H = 8192, 14
@@ -262,17 +319,17 @@ def bench_pointwise(pkg, device) -> dict:
     k_int = pkg.make_qk_norm_rope_interleaved()
     k_rh = pkg.make_qk_norm_rope()
     nbytes = 2 * T * H * 128 * 2 + T * 64 * 2 * 2 + 128 * 2
-    ms = time_graph([lambda x=x, o=o: k_int(x, w, 1e-6, table64[:, :64], table64[:, 64:], o) for x, o in zip(xs, outs)])
+    ms = timed([lambda x=x, o=o: k_int(x, w, 1e-6, table64[:, :64], table64[:, 64:], o) for x, o in zip(xs, outs)])
     record("qk_norm_rope_interleaved", ms, nbytes, [T, 1, H, 128])
     nbytes = 2 * T * H * 128 * 2 + T * 48 * 2 * 2 + 128 * 2
-    ms = time_graph([lambda x=x, o=o: k_rh(x, w, 1e-6, table48[:, :48], table48[:, 48:], o) for x, o in zip(xs, outs)])
+    ms = timed([lambda x=x, o=o: k_rh(x, w, 1e-6, table48[:, :48], table48[:, 48:], o) for x, o in zip(xs, outs)])
     record("qk_norm_rope", ms, nbytes, [T, 1, H, 128])
     # q and k in one pass (the fused QK-RMSNorm + 3D RoPE workload: 2 x 58.7 MB
     # of head rows + the [8192, 64] x 2 table + two weights).
     k_qk = pkg.make_qk_norm_rope_interleaved_qk()
     w2 = rnd(128, scale=0.1) + 1
     nbytes = 4 * T * H * 128 * 2 + T * 64 * 2 * 2 + 2 * 128 * 2
-    ms = time_graph([lambda i=i: k_qk(xs[2 * i], xs[2 * i + 1], w, w2, 1e-6, table64[:, :64], table64[:, 64:],
+    ms = timed([lambda i=i: k_qk(xs[2 * i], xs[2 * i + 1], w, w2, 1e-6, table64[:, :64], table64[:, 64:],
                                       outs[2 * i], outs[2 * i + 1]) for i in range(rot // 2)])
     record("qk_norm_rope_interleaved_qk", ms, nbytes, [2, T, 1, H, 128])
     ceiling("qk_norm_rope_interleaved_qk", 2 * T * H * 128 * 2, 1, 1, None)
@@ -286,7 +343,7 @@ def bench_pointwise(pkg, device) -> dict:
     positions = torch.randperm(T, device=device)
     k_pack = pkg.make_qkv_norm_rope_pack()
     nbytes = 6 * T * H * 128 * 2 + T * 8 + T * 96 * 2 + 2 * 128 * 2
-    ms = time_graph([lambda i=i, o=o: k_pack(*i, w, w, 1e-6, table48, positions, *o) for i, o in views])
+    ms = timed([lambda i=i, o=o: k_pack(*i, w, w, 1e-6, table48, positions, *o) for i, o in views])
     record("qkv_norm_rope_pack", ms, nbytes, [T, 1, H, 128])
     # The same with the fp8 epilogue: q and k leave as e4m3 codes.
     codes = [torch.empty(2, 1, T, H, 128, dtype=torch.float8_e4m3fn, device=device) for _ in range(3)]
@@ -294,20 +351,20 @@ def bench_pointwise(pkg, device) -> dict:
     views8 = [(i, [c[0].permute(1, 0, 2, 3), c[1].permute(1, 0, 2, 3), o[2]]) for (i, o), c in zip(views, codes)]
     k_pack8 = pkg.make_qkv_norm_rope_pack_fp8()
     nbytes = 3 * T * H * 128 * 2 + 2 * T * H * 128 + T * H * 128 * 2 + T * 8 + T * 96 * 2 + 2 * 128 * 2
-    ms = time_graph([lambda i=i, o=o: k_pack8(*i, w, w, 1e-6, table48, positions, *o, descales[0], descales[1])
+    ms = timed([lambda i=i, o=o: k_pack8(*i, w, w, 1e-6, table48, positions, *o, descales[0], descales[1])
                      for i, o in views8])
     record("qkv_norm_rope_pack_fp8", ms, nbytes, [T, 1, H, 128])
     # The same with V's per-head amax folded into slots while v is copied.
     k_pack8v = pkg.make_qkv_norm_rope_pack_fp8_vamax()
     v_amax = torch.empty(H, 64, device=device)
-    ms = time_graph([lambda i=i, o=o: k_pack8v(*i, w, w, 1e-6, table48, positions, *o, descales[0], descales[1],
+    ms = timed([lambda i=i, o=o: k_pack8v(*i, w, w, 1e-6, table48, positions, *o, descales[0], descales[1],
                                                 v_amax) for i, o in views8])
     record("qkv_norm_rope_pack_fp8_vamax", ms, nbytes, [T, 1, H, 128])
     # The same with two-term q and k codes (the fp8 configuration's recipe): lo codes beside the hi ones.
     codes_lo = [torch.empty(2, 1, T, H, 128, dtype=torch.float8_e4m3fn, device=device) for _ in range(3)]
     k_pack8x2 = pkg.make_qkv_norm_rope_pack_fp8x2_vamax()
     nbytes2 = nbytes + 2 * T * H * 128
-    ms = time_graph([lambda i=i, o=o, c=c: k_pack8x2(*i, w, w, 1e-6, table48, positions, o[0],
+    ms = timed([lambda i=i, o=o, c=c: k_pack8x2(*i, w, w, 1e-6, table48, positions, o[0],
                                                       c[0].permute(1, 0, 2, 3), o[1], c[1].permute(1, 0, 2, 3), o[2],
                                                       descales[0], descales[1], v_amax)
                      for (i, o), c in zip(views8, codes_lo)])
@@ -325,15 +382,15 @@ def bench_pointwise(pkg, device) -> dict:
     shift = rnd(1, 1, C, scale=0.1).expand(1, S, C)
     gate = rnd(1, 1, C, scale=0.1).expand(1, S, C)
     k_mod = pkg.make_rms_modulate()
-    ms = time_graph([lambda x=x, o=o: k_mod(x, wC, 1e-6, scale, shift, o) for x, o in zip(xs, outs)])
+    ms = timed([lambda x=x, o=o: k_mod(x, wC, 1e-6, scale, shift, o) for x, o in zip(xs, outs)])
     record("rms_modulate", ms, 2 * S * C * 2 + 3 * C * 2, [1, S, C])
     ceiling("rms_modulate", S * C * 2, 1, 1, C * 2)
     k_gr = pkg.make_gated_residual()
-    ms = time_graph([lambda x=x, y=y, o=o: k_gr(x, gate, y, o) for x, y, o in zip(xs, ys, outs)])
+    ms = timed([lambda x=x, y=y, o=o: k_gr(x, gate, y, o) for x, y, o in zip(xs, ys, outs)])
     record("gated_residual", ms, 3 * S * C * 2 + C * 2, [1, S, C])
     ceiling("gated_residual", S * C * 2, 2, 1, None)
     k_grm = pkg.make_gated_residual_rms_modulate()
-    ms = time_graph([lambda x=x, y=y, o=o, r=r: k_grm(x, gate, y, wC, 1e-6, scale, shift, r, o)
+    ms = timed([lambda x=x, y=y, o=o, r=r: k_grm(x, gate, y, wC, 1e-6, scale, shift, r, o)
                      for x, y, o, r in zip(xs, ys, outs, res)])
     record("gated_residual_rms_modulate", ms, 4 * S * C * 2 + 4 * C * 2, [1, S, C])
     ceiling("gated_residual_rms_modulate", S * C * 2, 2, 2, C * 2)
@@ -345,14 +402,14 @@ def bench_pointwise(pkg, device) -> dict:
     index = index.to(device).view(1, S)
     tables = R * C * 2
     k_mod_i = pkg.make_rms_modulate_indexed(check_indices=False)
-    ms = time_graph([lambda x=x, o=o: k_mod_i(x, wC, 1e-6, cols["scale_msa"], cols["shift_msa"], index, o)
+    ms = timed([lambda x=x, o=o: k_mod_i(x, wC, 1e-6, cols["scale_msa"], cols["shift_msa"], index, o)
                      for x, o in zip(xs, outs)])
     record("rms_modulate_indexed", ms, 2 * S * C * 2 + C * 2 + 2 * tables + S * 8, [1, S, C])
     k_gr_i = pkg.make_gated_residual_indexed(check_indices=False)
-    ms = time_graph([lambda x=x, y=y, o=o: k_gr_i(x, cols["gate_mlp"], y, index, o) for x, y, o in zip(xs, ys, outs)])
+    ms = timed([lambda x=x, y=y, o=o: k_gr_i(x, cols["gate_mlp"], y, index, o) for x, y, o in zip(xs, ys, outs)])
     record("gated_residual_indexed", ms, 3 * S * C * 2 + tables + S * 8, [1, S, C])
     k_grm_i = pkg.make_gated_residual_rms_modulate_indexed(check_indices=False)
-    ms = time_graph([lambda x=x, y=y, o=o, r=r: k_grm_i(x, cols["gate_msa"], y, wC, 1e-6, cols["scale_mlp"],
+    ms = timed([lambda x=x, y=y, o=o, r=r: k_grm_i(x, cols["gate_msa"], y, wC, 1e-6, cols["scale_mlp"],
                                                         cols["shift_mlp"], index, r, o)
                      for x, y, o, r in zip(xs, ys, outs, res)])
     record("gated_residual_rms_modulate_indexed", ms, 4 * S * C * 2 + C * 2 + 3 * tables + S * 8, [1, S, C])
@@ -361,7 +418,7 @@ def bench_pointwise(pkg, device) -> dict:
     gates = [rnd(1, S, F) for _ in range(2)]
     outs = [torch.empty_like(u) for u in ups]
     k_sw = pkg.make_swiglu()
-    ms = time_graph([lambda u=u, g=g, o=o: k_sw(u, g, o) for u, g, o in zip(ups, gates, outs)])
+    ms = timed([lambda u=u, g=g, o=o: k_sw(u, g, o) for u, g, o in zip(ups, gates, outs)])
     record("swiglu", ms, 3 * S * F * 2, [1, S, F])
     del ups, gates, outs
     ceiling("swiglu", S * F * 2, 2, 1, None)
