@@ -498,7 +498,9 @@ void rms_staged_kernel(RmsArgs a) {
 // there already; a group across a run boundary reads each row's factor and
 // shift from the tables (L2) instead. The launch bound keeps two blocks
 // resident per CU up to G = 14 (W = 7168).
-template <int G, int THREADS>
+//
+// EXACT: W8 = 64 G, so no group is clamped or masked.
+template <int G, int THREADS, bool EXACT>
 __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed_kernel(RmsArgs a) {
     constexpr int kWaves = THREADS / 64;
     static_assert((kWaves & (kWaves - 1)) == 0 && kWaves <= 64, "a power-of-two number of waves");
@@ -513,8 +515,11 @@ __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed
     U4 v[G];
     auto load_row = [&](int64_t b, int64_t s) {
 #pragma unroll
-        for (int k = 0; k < G; ++k) v[k] = ld16_stream(row_ptr(a.x, b, s) + clamp_group(lane + 64 * k, W8) * 8);
-        __builtin_amdgcn_sched_barrier(0);  // the row's loads stay together, ahead of its arithmetic
+        for (int k = 0; k < G; ++k)
+            v[k] = ld16_stream(row_ptr(a.x, b, s) + (EXACT ? lane + 64 * k : clamp_group(lane + 64 * k, W8)) * 8);
+        // The row's loads stay together, ahead of its arithmetic (EXACT's
+        // constant offsets keep them together without the barrier).
+        if constexpr (!EXACT) __builtin_amdgcn_sched_barrier(0);
     };
     int64_t in_lds = -1;
     for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWaves; base < a.rows; base += step) {
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed
 #pragma unroll
         for (int k = 0; k < G; ++k) {
             const U4 unused{};
-            v[k] = rms_phase1<kRmsModulate>(v[k], unused, unused, lane + 64 * k < W8, part[k & 3]);
+            v[k] = rms_phase1<kRmsModulate>(v[k], unused, unused, EXACT || lane + 64 * k < W8, part[k & 3]);
             keep_packed(v[k]);
         }
         const float total = (fold_lanes<64>(part[0]) + fold_lanes<64>(part[2])) +
@@ -564,18 +569,18 @@ __global__ __launch_bounds__(THREADS, G <= 14 ? 4 : 3) void rms_modulate_indexed
         if (same) {
 #pragma unroll
             for (int k = 0; k < G; ++k) {
-                const int g = lane + 64 * k, gc = clamp_group(g, W8);
+                const int g = lane + 64 * k, gc = EXACT ? g : clamp_group(g, W8);
                 const U4 o = rms_phase2<kRmsModulate>(v[k], r, lw[gc], lk[gc], lsh[gc]);
-                if (ok && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+                if (ok && (EXACT || g < W8)) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
             }
         } else {
 #pragma unroll
             for (int k = 0; k < G; ++k) {
-                const int g = lane + 64 * k, gc = clamp_group(g, W8);
+                const int g = lane + 64 * k, gc = EXACT ? g : clamp_group(g, W8);
                 const U4 kv = factor_of(ld16(row_ptr(a.scale, mine, 0) + gc * 8));
                 const U4 shv = ld16(row_ptr(a.shift, mine, 0) + gc * 8);
                 const U4 o = rms_phase2<kRmsModulate>(v[k], r, lw[gc], kv, shv);
-                if (ok && g < W8) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
+                if (ok && (EXACT || g < W8)) st16_stream(row_ptr_w(a.out, b, s) + g * 8, o);
                 __builtin_amdgcn_sched_barrier(0);  // one group's table loads at a time (registers)
             }
         }
@@ -765,11 +770,15 @@ int launch_rms_vec(const RmsArgs &a, hipStream_t stream) {
         if (MODE == kRmsModulate && a.index.p != nullptr && lds <= 65536 && need <= 16) {
             constexpr int kWaves = kStagedThreads / 64;
             const int64_t groups = (a.rows + kWaves - 1) / kWaves;
+            const bool exact = W8 % 64 == 0;
             const unsigned grid = static_cast<unsigned>(groups < kStagedBlocks ? groups : kStagedBlocks);
-#define H3_RMS_MOD_INDEXED(GG)                                                                              \
-    if (need <= GG) {                                                                                      \
-        rms_modulate_indexed_kernel<GG, kStagedThreads><<<grid, kStagedThreads, lds, stream>>>(a);         \
-        return launch_status();                                                                            \
+#define H3_RMS_MOD_INDEXED(GG)                                                                                    \
+    if (need <= GG) {                                                                                            \
+        if (exact && W8 == 64 * GG)                                                                              \
+            rms_modulate_indexed_kernel<GG, kStagedThreads, true><<<grid, kStagedThreads, lds, stream>>>(a);    \
+        else                                                                                                     \
+            rms_modulate_indexed_kernel<GG, kStagedThreads, false><<<grid, kStagedThreads, lds, stream>>>(a);   \
+        return launch_status();                                                                                  \
     }
             H3_RMS_MOD_INDEXED(2) H3_RMS_MOD_INDEXED(3) H3_RMS_MOD_INDEXED(4) H3_RMS_MOD_INDEXED(6)
             H3_RMS_MOD_INDEXED(8) H3_RMS_MOD_INDEXED(10) H3_RMS_MOD_INDEXED(12) H3_RMS_MOD_INDEXED(14)
