@@ -103,7 +103,25 @@ struct AttnArgs {
     // j: key tiles [p T / split, (p + 1) T / split) of the unit's T tiles.
     int n_full, n_tail, split;
     float *ws;                            // the partials (layout at kWsSlotAcc)
+    // SMALL kernels: workgroups [0, n_big) run 256-query units and workgroups
+    // [n_big, n_big + n_small) 192-query units, each range XCD-remapped on its
+    // own, so the 192-query units make up the last round. A head (b H + h)
+    // starts with its 256-query units and ends with its 192-query ones: heads
+    // 0 .. sm_k-1 hold sm_big0 and sm_small0 of them, head sm_k sm_big1 and
+    // sm_small1, the others qblocks 256-query units. Units are numbered head
+    // by head within each range.
+    int n_big, n_small, sm_k, sm_big0, sm_small0, sm_big1, sm_small1;
 };
+
+constexpr int kSmallBM = 192;  // queries of a SMALL launch's last-round units
+
+struct SmallUnit {
+    int bh, q0;  // head (b H + h) and first query
+    bool small;  // a 192-query unit
+};
+
+// The unit of SMALL workgroup x.
+__device__ __forceinline__ SmallUnit small_plan_unit(const AttnArgs &a, int x);
 
 // Workspace of the SPLIT kernels, per piece slot (u split + p): the
 // unnormalised O as [256 queries][128 dims] floats, then, after all slots'
@@ -128,6 +146,23 @@ __device__ __forceinline__ int xcd_remap(int x, int total) {
     const int per = total / 8, rem = total % 8;
     const int xcd = x % 8, slot = x / 8;
     return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+__device__ __forceinline__ SmallUnit small_plan_unit(const AttnArgs &a, int x) {
+    if (x < a.n_big) {
+        int i = xcd_remap(x, a.n_big);
+        const int c0 = a.sm_k * a.sm_big0;
+        if (i < c0) return {i / a.sm_big0, (i % a.sm_big0) * kBM, false};
+        i -= c0;
+        if (i < a.sm_big1) return {a.sm_k, i * kBM, false};
+        i -= a.sm_big1;
+        return {a.sm_k + 1 + i / a.qblocks, (i % a.qblocks) * kBM, false};
+    }
+    int i = xcd_remap(x - a.n_big, a.n_small);
+    const int c0 = a.sm_k * a.sm_small0;
+    if (i < c0) return {i / a.sm_small0, a.sm_big0 * kBM + (i % a.sm_small0) * kSmallBM, true};
+    i -= c0;
+    return {a.sm_k, a.sm_big1 * kBM + i * kSmallBM, true};
 }
 
 // Thread t's share of a 64-key tile: wave w's i-th load (i < kLoadRows) fills
@@ -602,12 +637,14 @@ __device__ __forceinline__ float fold_groups_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// S^T of one 64-key tile. kidx: this lane's K operand element for k-step 0
-// (row 16 kb + l % 16 of the tile, chunk 4 ks + l / 16; k-step ks reads
-// kidx ^ 32 ks). Each K operand feeds both query blocks.
-__device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qreg)[2][4], int kidx, f32x4_t (&s)[2][4]) {
+// S^T of one 64-key tile for NQB 16-query blocks. kidx: this lane's K operand
+// element for k-step 0 (row 16 kb + l % 16 of the tile, chunk 4 ks + l / 16;
+// k-step ks reads kidx ^ 32 ks). Each K operand feeds every query block.
+template <int NQB>
+__device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qreg)[NQB][4], int kidx,
+                                          f32x4_t (&s)[NQB][4]) {
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -618,7 +655,7 @@ __device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qre
         for (int kb = 0; kb < 4; ++kb) {
             const bf16x8_t kop = as_bf16x8(*reinterpret_cast<const uint4 *>(kt + 16 * kb * kRow + (kidx ^ (32 * ks))));
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
+            for (int qb = 0; qb < NQB; ++qb)
                 s[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qreg[qb][ks], s[qb][kb], 0, 0, 0);
         }
     // Rolling window of K operand reads, three ahead of the MFMAs (measured
@@ -626,10 +663,10 @@ __device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qre
     __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
 #pragma unroll
     for (int i = 0; i < 13; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 3 * NQB, 0);
 }
 
 // p = bf16(exp2(c s - m)) (keys >= valid: 0 when MASK), this lane's share of
@@ -637,12 +674,12 @@ __device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qre
 // vidx: this lane's V^T operand address for dim block 0 of the lower 4 keys
 // (row 4 (l / 16) + (l % 16) / 4, dims 4 (l % 4) of the block; block db reads
 // vidx ^ 16 db, the upper 4 keys 16 rows further, half h 32 rows further).
-template <bool MASK>
-__device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x4_t (&s)[2][4], const float (&m)[2],
-                                          float (&l)[2], float c, int valid, int g, f32x4_t (&acc)[2][8]) {
-    bf16x8_t pop[2][2];
+template <bool MASK, int NQB>
+__device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x4_t (&s)[NQB][4], const float (&m)[NQB],
+                                          float (&l)[NQB], float c, int valid, int g, f32x4_t (&acc)[NQB][8]) {
+    bf16x8_t pop[NQB][2];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NQB; ++qb) {
         float p[4][4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
@@ -684,32 +721,33 @@ __device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x
             const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
             const bf16x8_t vop = as_bf16x8(make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
+            for (int qb = 0; qb < NQB; ++qb)
                 acc[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[qb][h], acc[qb][db], 0, 0, 0);
         }
     // Rolling window of V^T operand reads (two per operand), two operands ahead.
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int i = 0; i < 14; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NQB, 0);
 }
 
 // A tile with the running-maximum rescale: the tile's maximum, and when it
 // raises the running maximum m of some query, O and the denominator scaled by
 // exp2(m_old - m_new) first (the reference's order). From m = -inf, l = 0,
 // O = 0 it sets the reference maximum of the first tile.
-template <bool MASK, bool NEG>
-__device__ __forceinline__ void exact_tile16(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[2][4],
-                                             int kidx, int vidx, int g, float c, float (&m)[2], float (&l)[2],
-                                             f32x4_t (&acc)[2][8]) {
-    f32x4_t s[2][4];
+template <bool MASK, bool NEG, int NQB>
+__device__ __forceinline__ void exact_tile16(const bf16_t *kt, const bf16_t *vt, int valid,
+                                             const bf16x8_t (&qreg)[NQB][4], int kidx, int vidx, int g, float c,
+                                             float (&m)[NQB], float (&l)[NQB], f32x4_t (&acc)[NQB][8]) {
+    static_assert(NQB == 1 || NQB == 2, "one or two query blocks per wave");
+    f32x4_t s[NQB][4];
     qk_tile16(kt, qreg, kidx, s);
-    float mt[2];
+    float mt[NQB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NQB; ++qb) {
         if constexpr (MASK) {
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
@@ -724,31 +762,45 @@ __device__ __forceinline__ void exact_tile16(const bf16_t *kt, const bf16_t *vt,
             for (int i = 0; i < 4; ++i) mx = NEG ? fminf(mx, s[qb][kb][i]) : fmaxf(mx, s[qb][kb][i]);
         mt[qb] = fold_groups_max<NEG>(mx) * c;
     }
-    const bool grow0 = mt[0] > m[0], grow1 = mt[1] > m[1];
-    if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
-        const float n0 = grow0 ? mt[0] : m[0], n1 = grow1 ? mt[1] : m[1];
-        const float a0 = __builtin_amdgcn_exp2f(m[0] - n0), a1 = __builtin_amdgcn_exp2f(m[1] - n1);
-        m[0] = n0;
-        m[1] = n1;
-        l[0] *= a0;
-        l[1] *= a1;
+    if constexpr (NQB == 2) {
+        const bool grow0 = mt[0] > m[0], grow1 = mt[1] > m[1];
+        if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
+            const float n0 = grow0 ? mt[0] : m[0], n1 = grow1 ? mt[1] : m[1];
+            const float a0 = __builtin_amdgcn_exp2f(m[0] - n0), a1 = __builtin_amdgcn_exp2f(m[1] - n1);
+            m[0] = n0;
+            m[1] = n1;
+            l[0] *= a0;
+            l[1] *= a1;
 #pragma unroll
-        for (int db = 0; db < 8; ++db)
+            for (int db = 0; db < 8; ++db)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[0][db][i] *= a0;
-                acc[1][db][i] *= a1;
-            }
+                for (int i = 0; i < 4; ++i) {
+                    acc[0][db][i] *= a0;
+                    acc[1][db][i] *= a1;
+                }
+        }
+    } else {
+        const bool grow0 = mt[0] > m[0];
+        if (__builtin_amdgcn_ballot_w64(grow0)) {
+            const float n0 = grow0 ? mt[0] : m[0];
+            const float a0 = __builtin_amdgcn_exp2f(m[0] - n0);
+            m[0] = n0;
+            l[0] *= a0;
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[0][db][i] *= a0;
+        }
     }
     pv_tile16<MASK>(vt, vidx, s, m, l, c, valid, g, acc);
 }
 
 // A tile against the fixed reference maximum m.
-template <bool MASK>
-__device__ __forceinline__ void ref_tile16(const bf16_t *kt, const bf16_t *vt, int valid, const bf16x8_t (&qreg)[2][4],
-                                           int kidx, int vidx, int g, float c, const float (&m)[2], float (&l)[2],
-                                           f32x4_t (&acc)[2][8]) {
-    f32x4_t s[2][4];
+template <bool MASK, int NQB>
+__device__ __forceinline__ void ref_tile16(const bf16_t *kt, const bf16_t *vt, int valid,
+                                           const bf16x8_t (&qreg)[NQB][4], int kidx, int vidx, int g, float c,
+                                           const float (&m)[NQB], float (&l)[NQB], f32x4_t (&acc)[NQB][8]) {
+    f32x4_t s[NQB][4];
     qk_tile16(kt, qreg, kidx, s);
     pv_tile16<MASK>(vt, vidx, s, m, l, c, valid, g, acc);
 }
@@ -960,6 +1012,186 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     }
 }
 
+// attention16_kernel for the launch whose last round is 192-query units (see
+// AttnArgs, SMALL kernels). In such a unit waves 0-3 take 32 queries each and
+// waves 4-7 16 each, so every SIMD (waves w and w + 4) carries 48 queries, 3/4
+// of a 256-query unit; the arithmetic of a query is attention16_kernel's. (A
+// kernel of its own: folding this plan into attention16_kernel changed that
+// kernel's code enough to raise its HBM traffic at S = 73,984 by 3-30%.)
+template <bool NEG>
+__global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4))) void attention16_small_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_k0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_k1[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_v0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t lds_v1[kTileElems];
+    __shared__ int wave_overflow[kWaves];
+
+    const SmallUnit u = small_plan_unit(a, static_cast<int>(blockIdx.x));
+    const int b = u.bh / a.H, h = u.bh % a.H;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // a scalar: the branch below is on it
+    const int l16 = lane & 15, g = lane >> 4;
+    const bf16_t *qbase = a.q + b * a.qs[0] + h * a.qs[1];
+    const bf16_t *kbase = a.k + b * a.ks[0] + h * a.ks[1];
+    const bf16_t *vbase = a.v + b * a.vs[0] + h * a.vs[1];
+    bf16_t *obase = a.o + b * a.os[0] + h * a.os[1];
+
+    // This wave's queries: NQB blocks of 16 from q_first (waves 4-7 of a
+    // 192-query unit: one block each, after the 128 queries of waves 0-3).
+    const int q_first = u.small && wave >= 4 ? u.q0 + 128 + 16 * (wave - 4) : u.q0 + 32 * wave;
+    auto run = [&](auto nqb_tag) __attribute__((always_inline)) {
+        constexpr int NQB = decltype(nqb_tag)::value;
+        // Q^T operands: query block qb, k-step ks holds dims 32 ks + 8 g .. +8 of
+        // query 16 qb + l16 of this wave's queries.
+        bf16x8_t qreg[NQB][4];
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            int query = q_first + 16 * qb + l16;
+            query = query < a.Sq ? query : a.Sq - 1;
+            const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qreg[qb][ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * g));
+            if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const uint4 u = __builtin_bit_cast(uint4, qreg[qb][ks]);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = pack2(lo2f(w[e]) * a.c, hi2f(w[e]) * a.c);
+                    qreg[qb][ks] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
+                }
+            }
+        }
+
+        const __amdgpu_buffer_rsrc_t krs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(kbase), static_cast<short>(0), a.k_bytes, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t vrs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(vbase), static_cast<short>(0), a.v_bytes, kBufferWord3);
+        int kvoff[kLoadRows], vvoff[kLoadRows];
+        const int kstep = static_cast<int>(a.ks[2]) * 2 * kBN, vstep = static_cast<int>(a.vs[2]) * 2 * kBN;
+#pragma unroll
+        for (int r = 0; r < kLoadRows; ++r) {
+            const int row = tile_row(r);
+            kvoff[r] = (row * static_cast<int>(a.ks[2]) + 8 * (static_cast<int>(threadIdx.x & 15) ^ swz_k(row))) * 2;
+            vvoff[r] = (row * static_cast<int>(a.vs[2]) + 8 * (static_cast<int>(threadIdx.x & 15) ^ swz_v16(row))) * 2;
+        }
+        const int kidx = l16 * kRow + 8 * (g ^ l16);
+        const int vrow = 4 * g + (l16 >> 2);
+        const int vidx = vrow * kRow + (16 * (vrow & 7) + 8 * ((l16 >> 1) & 1) + 4 * (l16 & 1));
+        const float c = a.prescale ? 1.0f : a.c;  // the logits' factor (1 when c is in bf16(c q))
+
+        // Key tiles [0, full) are full; a partial tile (Sk % 64 keys) follows.
+        const int T = (a.Sk + kBN - 1) / kBN, full = a.Sk / kBN;
+        constexpr int t0 = 0;
+        const int t_end = full;
+        const bool partial = full < T;
+        const int valid_last = a.Sk - full * kBN;
+
+        f32x4_t acc[NQB][8];
+        float m[NQB], l[NQB];
+        // One pass over the unit's tiles: the first exact (it sets the reference
+        // maxima), the rest against them (EXACT: all with the online rescale).
+        auto pass = [&](auto exact_tag) __attribute__((always_inline)) {
+            constexpr bool EXACT = decltype(exact_tag)::value;
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                m[qb] = -INFINITY;
+                l[qb] = 0.0f;
+#pragma unroll
+                for (int db = 0; db < 8; ++db)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[qb][db][i] = 0.0f;
+            }
+            dma_tile(krs, kvoff, t0 * kstep, lds_k0);
+            dma_tile(vrs, vvoff, t0 * vstep, lds_v0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            // Tile `tile` from (kc, vc) while tile + 1 is loaded into (kn, vn);
+            // past the head's last key the loads read zeros (unused).
+            auto step = [&](auto first_tag, int tile, const bf16_t *kc, const bf16_t *vc, bf16_t *kn, bf16_t *vn)
+                            __attribute__((always_inline)) {
+                dma_tile(krs, kvoff, (tile + 1) * kstep, kn);
+                dma_tile(vrs, vvoff, (tile + 1) * vstep, vn);
+                if constexpr (EXACT || decltype(first_tag)::value)
+                    exact_tile16<false, NEG>(kc, vc, kBN, qreg, kidx, vidx, g, c, m, l, acc);
+                else
+                    ref_tile16<false>(kc, vc, kBN, qreg, kidx, vidx, g, c, m, l, acc);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            };
+            if (t_end > t0) {
+                step(std::true_type{}, t0, lds_k0, lds_v0, lds_k1, lds_v1);
+                int t = t0 + 1;
+                for (; t + 1 < t_end; t += 2) {
+                    step(std::false_type{}, t, lds_k1, lds_v1, lds_k0, lds_v0);
+                    step(std::false_type{}, t + 1, lds_k0, lds_v0, lds_k1, lds_v1);
+                }
+                if (t < t_end) step(std::false_type{}, t, lds_k1, lds_v1, lds_k0, lds_v0);
+                if (partial) {  // tile t_end, in buffer (t_end - t0) & 1
+                    const bool odd = (t_end - t0) & 1;
+                    const bf16_t *kc = odd ? lds_k1 : lds_k0;
+                    const bf16_t *vc = odd ? lds_v1 : lds_v0;
+                    if constexpr (EXACT)
+                        exact_tile16<true, NEG>(kc, vc, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                    else
+                        ref_tile16<true>(kc, vc, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                }
+            } else if (partial) {  // the partial tile is the only one
+                exact_tile16<true, NEG>(lds_k0, lds_v0, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+            }
+        };
+        pass(std::false_type{});
+        // Overflow against the reference maxima: redo the unit with the running
+        // maximum (as attention16_kernel does).
+        float lt[NQB];
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) lt[qb] = fold_groups_sum(l[qb]);
+        constexpr float limit = INFINITY;
+        // x < limit is false for NaN, so NaN counts as overflow too.
+        bool finite = true;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) finite = finite && lt[qb] < limit;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) finite = finite && fabsf(acc[qb][db][i]) < limit;
+        const bool wave_bad = __builtin_amdgcn_ballot_w64(!finite) != 0;
+        if (lane == 0) wave_overflow[wave] = wave_bad ? 1 : 0;
+        __syncthreads();
+        int any_bad = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) any_bad |= wave_overflow[w];
+        if (any_bad) {
+            pass(std::true_type{});
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) lt[qb] = fold_groups_sum(l[qb]);
+        }
+        // o = acc / denominator, bf16: lane l holds dims 16 db + 4 g .. +4 of
+        // query 16 qb + l16.
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const int query = q_first + 16 * qb + l16;
+            if (query >= a.Sq) continue;
+            const float inv = __fdiv_rn(1.0f, lt[qb]);
+            bf16_t *orow = obase + static_cast<int64_t>(query) * a.os[2];
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                uint2 w;
+                w.x = pack2(acc[qb][db][0] * inv, acc[qb][db][1] * inv);
+                w.y = pack2(acc[qb][db][2] * inv, acc[qb][db][3] * inv);
+                *reinterpret_cast<uint2 *>(orow + 16 * db + 4 * g) = w;
+            }
+        }
+    };
+    if (u.small && wave >= 4)
+        run(std::integral_constant<int, 1>{});
+    else
+        run(std::integral_constant<int, 2>{});
+}
+
 // Combines the SPLIT pieces of the tail units: a 256-thread block per (tail
 // unit, 8 queries), a thread per (query, 4 dims), all SPLIT pieces' loads
 // issued together. With M = max_p m_p and w_p = 2^(m_p - M):
@@ -1080,6 +1312,42 @@ SplitPlan plan_split(int64_t units, int64_t tiles, int n_cu) {
     return plan;
 }
 
+// A last round of t 256-query units (t / n_cu at most 3/4) run instead as
+// 4t/3 units of 192 queries: each CU of that round carries 3/4 of a unit, and
+// the round fills the CUs. Three of every four 256-query units of a head's
+// tail become four 192-query units (the same queries); the plan spreads those
+// conversions over as few heads as it can (each head gives at most a third of
+// its units). Taken when Sq is a multiple of 256, t is a multiple of 3 and the
+// new round keeps at least kRoundFloor of the CUs busy, so it costs 3/4 of a
+// round where the unsplit tail costs max(t / n_cu, kRoundFloor). No workspace;
+// each query's arithmetic is that of the unsplit launch.
+struct SmallPlan {
+    bool use = false;
+    int n_big = 0, n_small = 0, k = 0, big0 = 0, small0 = 0, big1 = 0, small1 = 0;
+};
+
+SmallPlan plan_small(int64_t heads, int64_t Sq, int n_cu) {
+    SmallPlan p;
+    if (n_cu <= 0 || heads <= 0 || Sq <= 0 || Sq % kBM != 0) return p;
+    const int64_t per_head = Sq / kBM, units = heads * per_head;
+    const int64_t rounds = units / n_cu, tail = units % n_cu;
+    if (rounds < 1 || tail == 0 || tail % 3 != 0) return p;
+    const int64_t n_small = 4 * tail / 3;
+    if (n_small > n_cu || static_cast<double>(n_small) < kRoundFloor * n_cu) return p;
+    const int64_t conversions = tail / 3, per_head_max = per_head / 3;
+    if (per_head_max == 0 || conversions > heads * per_head_max) return p;
+    const int64_t rem = conversions % per_head_max;
+    p.use = true;
+    p.n_big = static_cast<int>(rounds * n_cu);
+    p.n_small = static_cast<int>(n_small);
+    p.k = static_cast<int>(conversions / per_head_max);
+    p.big0 = static_cast<int>(per_head - 3 * per_head_max);
+    p.small0 = static_cast<int>(4 * per_head_max);
+    p.big1 = static_cast<int>(per_head - 3 * rem);
+    p.small1 = static_cast<int>(4 * rem);
+    return p;
+}
+
 
 // The launcher of both numerics: fp32_qk (logits scaled by c = scale log2 e in
 // fp32) and bf16_prescale (q rounded to bf16(c q) before the product).
@@ -1154,11 +1422,31 @@ int launch_attention(NineToothedStream stream, NineToothedTensor q, NineToothedT
     const unsigned g = static_cast<unsigned>(grid);
     hipStream_t st = as_stream(stream);
     const bool neg = a.c < 0.0f && !prescale;  // the loop's max runs over c * s
-    if (workspace != nullptr && buf && dim == kD && !prescale && wv.shape[0] > 0) {
+    int n_cu = 0;
+    if (buf && dim == kD) {
         int dev = 0;
         const hipError_t e = hipStreamGetDevice(st, &dev);
         if (e != hipSuccess) return static_cast<int>(e);
-        const SplitPlan plan = plan_split(grid, (a.Sk + kBN - 1) / kBN, device_cus(dev));
+        n_cu = device_cus(dev);
+        const SmallPlan sp = plan_small(static_cast<int64_t>(a.B) * a.H, a.Sq, n_cu);
+        if (sp.use) {
+            a.n_big = sp.n_big;
+            a.n_small = sp.n_small;
+            a.sm_k = sp.k;
+            a.sm_big0 = sp.big0;
+            a.sm_small0 = sp.small0;
+            a.sm_big1 = sp.big1;
+            a.sm_small1 = sp.small1;
+            const unsigned gs = static_cast<unsigned>(sp.n_big + sp.n_small);
+            if (neg)
+                attention16_small_kernel<true><<<gs, kThreadsWG, 0, st>>>(a);
+            else
+                attention16_small_kernel<false><<<gs, kThreadsWG, 0, st>>>(a);
+            return launch_status();
+        }
+    }
+    if (workspace != nullptr && buf && dim == kD && !prescale && wv.shape[0] > 0) {
+        const SplitPlan plan = plan_split(grid, (a.Sk + kBN - 1) / kBN, n_cu);
         const int64_t pieces = static_cast<int64_t>(plan.n_tail) * plan.split;
         if (plan.split > 1 && wv.shape[0] >= pieces * kWsSlotBytes) {
             a.n_full = plan.n_full;
@@ -1220,6 +1508,7 @@ extern "C" int64_t h3_full_attention_workspace_bytes(int64_t B, int64_t H, int64
     if (hipGetDevice(&dev) != hipSuccess) return -1;
     const int64_t units = B * H * ((Sq + kBM - 1) / kBM);
     if (units > std::numeric_limits<int32_t>::max()) return 0;
+    if (plan_small(B * H, Sq, device_cus(dev)).use) return 0;  // the 192-query last round needs none
     const SplitPlan plan = plan_split(units, (Sk + kBN - 1) / kBN, device_cus(dev));
     return plan.split > 1 ? static_cast<int64_t>(plan.n_tail) * plan.split * kWsSlotBytes : 0;
 }

@@ -507,9 +507,9 @@ def test_attention_split_last_round(pkg, device, B, H, Sq, Sk, sign, outliers):
 
 def test_attention_split_plan_leaves_a_three_quarter_round(pkg, device):
     """At S = 8192, H = 14 (448 units on 256 CUs) the last round is 3/4 full:
-    the busy CUs clock up by about what the idle quarter costs, so the plan
-    does not split it; the configuration at S = 73,984 (a 4/5-full last round
-    of 16) is not split either. At S = 12,288 (672 units: a 5/8-full last
+    it runs as a round of 192-query units, which needs no workspace; the
+    configuration at S = 73,984 (a 4/5-full last round of 16) is not split
+    either. At S = 12,288 (672 units: a 5/8-full last
     round) it splits, which measured 3.4% faster (848.5 against 877.8 us)."""
     if torch.cuda.get_device_properties(device).multi_processor_count != 256:
         pytest.skip("the plan is stated for 256 CUs")
@@ -544,6 +544,70 @@ def test_attention_ws_small_workspace_runs_unsplit(pkg, device):
     torch.cuda.synchronize()
     assert not torch.equal(out, ref) and not torch.isnan(out).any()
     assert attention_error(out, ref.float())[1] <= 5e-3
+
+
+# ------------------------------------------------------------ 192-query last round
+
+def _attention16_launched(fn):
+    """The D = 128 attention kernels `fn` launches, as name<template args>."""
+    from torch.profiler import ProfilerActivity, profile
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    return sorted({"attention16" + e.name.split("attention16")[1].split(">")[0] + ">"
+                   for e in prof.events() if "attention16" in e.name})
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,scale,entry,case", [
+    (1, 14, 8192, 8192, 128 ** -0.5, "launch_h3_full_attention", "config"),
+    (1, 14, 8192, 5000, -0.07, "launch_h3_full_attention", "partial key tile, negative scale"),
+    (2, 14, 4096, 4096, 128 ** -0.5, "launch_h3_full_attention", "B = 2"),
+    (20, 16, 768, 700, 0.09, "launch_h3_full_attention", "64 heads all 192-query, one all 256"),
+    (1, 14, 8192, 8192, 128 ** -0.5, "launch_h3_full_attention_bf16_prescale", "prescale"),
+    (1, 14, 8192, 8192, 128 ** -0.5, "launch_h3_full_attention", "overflow in 192-query units"),
+])
+def test_attention_192_query_last_round(pkg, device, B, H, Sq, Sk, scale, entry, case):
+    """A launch whose last round of 256-query units would leave a quarter of
+    the CUs idle (448 units on 256 CUs at S = 8192, H = 14) runs that round as
+    256 units of 192 queries instead (waves 0-3 with 32 queries, waves 4-7 with
+    16). Each query's arithmetic is that of the ordinary launch, so one launch
+    over all heads equals launches of one head each (which are too small for
+    the plan) bitwise, whatever unit a query lands in. The 'overflow' case
+    puts a key ~200 log2 units above the first tile's maximum for every query
+    of head 0, most of whose queries lie in 192-query units: every workgroup
+    of that head takes the exact fallback, in both launches."""
+    if torch.cuda.get_device_properties(device).multi_processor_count != 256:
+        pytest.skip("the plan is stated for 256 CUs")
+    L = pkg._lib
+    gen = torch.Generator("cpu").manual_seed(Sq + Sk + B * H)
+    q = torch.randn(B, H, Sq, 128, generator=gen)
+    k = torch.randn(B, H, Sk, 128, generator=gen)
+    v = torch.randn(B, H, Sk, 128, generator=gen)
+    if case.startswith("overflow"):
+        q[0, 0, :, 0] = 16.0
+        k[0, 0, :, 0] *= 0.1
+        k[0, 0, 4000, 0] = 100.0  # a logit ~204 log2 units up, in tile 62
+    q, k, v = (t.to(BF).to(device) for t in (q, k, v))
+    stream = torch.cuda.current_stream(device).cuda_stream
+    print(f"192-query round: {case} B={B} H={H} Sq={Sq} Sk={Sk} {entry}", flush=True)
+    out = torch.full_like(q, float("nan"))
+    launched = _attention16_launched(
+        lambda: L.call(entry, stream, L.tensor(q), L.tensor(k), L.tensor(v), L.scalar(scale), L.tensor(out)))
+    neg = "true" if scale < 0 and "prescale" not in entry else "false"
+    assert launched == [f"attention16_small_kernel<{neg}>"], launched
+    ref = torch.full_like(q, float("nan"))
+    for b in range(B):
+        for h in range(H):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            assert L.call(entry, stream, L.tensor(q[sl]), L.tensor(k[sl]), L.tensor(v[sl]), L.scalar(scale),
+                          L.tensor(ref[sl])) == 0
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    assert torch.equal(out, ref), int((out != ref).sum())
+    if case.startswith("overflow"):
+        head0 = out[0, 0].float()
+        assert torch.isfinite(head0).all()
+        assert float((head0 - v[0, 0, 4000].float()).abs().max()) <= 2e-2
 
 
 @pytest.mark.parametrize("S,outliers", [(73984, 0.01), (16384, 0.0)])
