@@ -49,12 +49,15 @@ typedef struct NineToothedTensor {
  * runs on an element-strided path with the same arithmetic. Sq may differ from
  * Sk (keys past Sk are masked). scale: fp64 scalar. fp32 logits scaled by
  * scale * log2(e), exp2, bf16 P for the P.V product. The softmax's
- * stabilising maximum is each 256-query unit's first key tile's maximum, kept
- * for the unit's later tiles (the unit is recomputed with the running
+ * stabilising maximum is each query's maximum over the first key tile, kept
+ * for the later tiles (a workgroup recomputes its queries with the running
  * maximum when anything overflows against it), and the denominator sums the
  * same bf16-rounded P that weights V; the reference instead rescales at every
  * new running maximum and sums P in fp32 before rounding (both orders stay
- * within the operator's tolerance).
+ * within the operator's tolerance). Queries run in units of 256 per
+ * workgroup; a launch whose last round of units would leave a quarter of the
+ * CUs idle runs that round as units of 192 queries (same per-query
+ * arithmetic). Allocates nothing.
  * Replaces launch_h3_full_attention (tools/h3_attention.py:25-41,104-121;
  * called at patches/InfiniCore.patch:1421-1422 with the [B,S,H,D] -> [B,H,S,D]
  * stride swap of :1403-1411). */
