@@ -16,11 +16,13 @@
 //     16-byte chunks are XOR-swizzled so every operand read is bank-conflict
 //     free (below); the next tile's loads run during the current tile's work;
 //   - one workgroup fills a CU, so a launch runs in rounds of one workgroup
-//     per CU. When the last round is only partly filled and a workspace is
-//     given, the units of that round are split along the keys into pieces
-//     that fill whole rounds (SPLIT); each piece leaves its unnormalised O,
-//     reference maximum and denominator in the workspace and a merge kernel
-//     combines them (the same algebra as the online rescale).
+//     per CU. When the last round would be about 2/3 to 3/4 full, it runs
+//     instead as a full round of 192-query units (attention16_small_kernel).
+//     When it is otherwise partly filled and a workspace is given, the units
+//     of that round are split along the keys into pieces that fill whole
+//     rounds (SPLIT); each piece leaves its unnormalised O, reference maximum
+//     and denominator in the workspace and a merge kernel combines them (the
+//     same algebra as the online rescale).
 //
 // attention16_kernel (D = 128 on the buffer path: the configurations) runs on
 // v_mfma_f32_16x16x32_bf16 and keeps one reference maximum per unit (its
