@@ -610,33 +610,31 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
 // sums p in fp32 before that rounding). Against a running maximum the largest
 // p of a row is exactly 1 and loses nothing to bf16; against a fixed m it is
 // any number, and a row that one key dominates would carry that key's bf16
-// rounding (up to 2^-9) into o if the denominator did not share it. With the
-// shared weights o is an exact convex combination of the V rows under the
-// rounded weights.
+// rounding (up to 2^-9) into o if the denominator did not share it (at
+// |o| ~ 8 that flips the bf16 rounding of o: 0.03 from the fp32 result on the
+// peaky configuration). With the shared weights o is an exact convex
+// combination of the V rows under the rounded weights. The sum runs on the
+// matrix core, as a product of a ones operand with P^T accumulated across
+// the tiles (4 products per tile and wave beside the 64 of Q K^T and P V):
+// the VALU sum it replaces, v_dot2c_f32_bf16 against (1, 1), issues about
+// four times slower than an fp32 add and cost 2-3% of the kernel's time.
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // V tile swizzle of this kernel: chunk c of row r at slot c ^ 2 (r & 7), so
 // the 8 consecutive rows x 2 chunks one half-wave's ds_read_b64_tr_b16 reads
 // land on 16 distinct slots.
 __device__ __forceinline__ int swz_v16(int row) { return 2 * (row & 7); }
 
-// Max (NEG: min) and sum over the four 16-lane groups that hold a query's
-// keys: lanes l, l ^ 16, l ^ 32, l ^ 48, combined as ((x0 . x1) . (x2 . x3))
-// in every one of them.
+// Max (NEG: min) over the four 16-lane groups that hold a query's keys: lanes
+// l, l ^ 16, l ^ 32, l ^ 48, combined as ((x0 . x1) . (x2 . x3)) in every one
+// of them.
 template <bool NEG>
 __device__ __forceinline__ float fold_groups_max(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     x = NEG ? fminf(__uint_as_float(a[0]), __uint_as_float(a[1])) : fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return NEG ? fminf(__uint_as_float(b[0]), __uint_as_float(b[1])) : fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float fold_groups_sum(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // S^T of one 64-key tile for NQB 16-query blocks. kidx: this lane's K operand
@@ -671,14 +669,14 @@ __device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qre
     __builtin_amdgcn_sched_group_barrier(0x008, 3 * NQB, 0);
 }
 
-// p = bf16(exp2(c s - m)) (keys >= valid: 0 when MASK), this lane's share of
-// the denominator (the same bf16 p, summed in fp32), and O^T += V^T P^T.
+// P = bf16(exp2(c s - m)) (keys >= valid: 0 when MASK), the denominator
+// l += sum of P, and O^T += V^T P^T.
 // vidx: this lane's V^T operand address for dim block 0 of the lower 4 keys
 // (row 4 (l / 16) + (l % 16) / 4, dims 4 (l % 4) of the block; block db reads
 // vidx ^ 16 db, the upper 4 keys 16 rows further, half h 32 rows further).
 template <bool MASK, int NQB>
 __device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x4_t (&s)[NQB][4], const float (&m)[NQB],
-                                          float (&l)[NQB], float c, int valid, int g, f32x4_t (&acc)[NQB][8]) {
+                                          f32x4_t (&l)[NQB], float c, int valid, int g, f32x4_t (&acc)[NQB][8]) {
     bf16x8_t pop[NQB][2];
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
@@ -693,10 +691,6 @@ __device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x
                 }
                 p[kb][i] = e;
             }
-        // The rounded p summed in four short chains, word e of both halves
-        // each (v_dot2c_f32_bf16 against (1, 1): + p0 + p1 per word), then
-        // (r0 + r1) + (r2 + r3) with r0 starting from l.
-        float r[4] = {l[qb], 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             uint4 packed;
@@ -705,13 +699,16 @@ __device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x
             packed.z = pack2(p[2 * h + 1][0], p[2 * h + 1][1]);
             packed.w = pack2(p[2 * h + 1][2], p[2 * h + 1][3]);
             pop[qb][h] = as_bf16x8(packed);
-            const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                r[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[e]),
-                                                       __builtin_bit_cast(bf16x2_t, 0x3f803f80u), r[e], false);
         }
-        l[qb] = (r[0] + r[1]) + (r[2] + r[3]);
+    }
+    // The denominator on the matrix core: ones x P^T adds the 32 keys of each
+    // half to every row of l (each lane then holds its query's whole sum).
+    {
+        const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) l[qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[qb][h], l[qb], 0, 0, 0);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -743,7 +740,7 @@ __device__ __forceinline__ void pv_tile16(const bf16_t *vt, int vidx, const f32x
 template <bool MASK, bool NEG, int NQB>
 __device__ __forceinline__ void exact_tile16(const bf16_t *kt, const bf16_t *vt, int valid,
                                              const bf16x8_t (&qreg)[NQB][4], int kidx, int vidx, int g, float c,
-                                             float (&m)[NQB], float (&l)[NQB], f32x4_t (&acc)[NQB][8]) {
+                                             float (&m)[NQB], f32x4_t (&l)[NQB], f32x4_t (&acc)[NQB][8]) {
     static_assert(NQB == 1 || NQB == 2, "one or two query blocks per wave");
     f32x4_t s[NQB][4];
     qk_tile16(kt, qreg, kidx, s);
@@ -801,10 +798,36 @@ __device__ __forceinline__ void exact_tile16(const bf16_t *kt, const bf16_t *vt,
 template <bool MASK, int NQB>
 __device__ __forceinline__ void ref_tile16(const bf16_t *kt, const bf16_t *vt, int valid,
                                            const bf16x8_t (&qreg)[NQB][4], int kidx, int vidx, int g, float c,
-                                           const float (&m)[NQB], float (&l)[NQB], f32x4_t (&acc)[NQB][8]) {
+                                           const float (&m)[NQB], f32x4_t (&l)[NQB], f32x4_t (&acc)[NQB][8]) {
     f32x4_t s[NQB][4];
     qk_tile16(kt, qreg, kidx, s);
     pv_tile16<MASK>(vt, vidx, s, m, l, c, valid, g, acc);
+}
+
+// A query's denominator: every row of its l accumulator holds the whole sum.
+__device__ __forceinline__ float den_total(const f32x4_t &l) { return l[0]; }
+
+// The Q^T operands of query block qb (k-step ks: dims 32 ks + 8 g .. +8 of
+// query q_first + 16 qb + l16, clamped to the last query), prescaled to
+// bf16(fp32(c) * fp32(q)) for the prescale numerics (tools/h3_attention.py:88).
+__device__ __forceinline__ void load_q16(const AttnArgs &a, const bf16_t *qbase, int q_first, int qb, int l16, int g,
+                                         bf16x8_t (&qr)[4]) {
+    int query = q_first + 16 * qb + l16;
+    query = query < a.Sq ? query : a.Sq - 1;
+    const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qr[ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * g));
+    if (a.prescale) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint4 u = __builtin_bit_cast(uint4, qr[ks]);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = pack2(lo2f(w[e]) * a.c, hi2f(w[e]) * a.c);
+            qr[ks] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
+        }
+    }
 }
 
 // SPLIT: the key-split launch (see AttnArgs); a piece leaves its unnormalised
@@ -844,25 +867,8 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     // query 16 qb + l16 of this wave's 32.
     const int q_first = qbk * kBM + wave * 32;
     bf16x8_t qreg[2][4];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        int query = q_first + 16 * qb + l16;
-        query = query < a.Sq ? query : a.Sq - 1;
-        const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qreg[qb][ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * g));
-        if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const uint4 u = __builtin_bit_cast(uint4, qreg[qb][ks]);
-                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-                uint32_t o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = pack2(lo2f(w[e]) * a.c, hi2f(w[e]) * a.c);
-                qreg[qb][ks] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
-            }
-        }
-    }
+    load_q16(a, qbase, q_first, 0, l16, g, qreg[0]);
+    load_q16(a, qbase, q_first, 1, l16, g, qreg[1]);
 
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(kbase), static_cast<short>(0), a.k_bytes, kBufferWord3);
@@ -897,19 +903,23 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
     const int valid_last = a.Sk - full * kBN;
 
     f32x4_t acc[2][8];
-    float m[2], l[2];
-    // One pass over the unit's tiles: the first exact (it sets the reference
-    // maxima), the rest against them (EXACT: all with the online rescale).
-    auto pass = [&](auto exact_tag) __attribute__((always_inline)) {
+    float m[2];
+    f32x4_t l[2];
+    // One pass over the unit's tiles for the query blocks of qq (one or two;
+    // their maxima, denominator chains and accumulators in mm, ll, aa): the
+    // first tile exact (it sets the reference maxima), the rest against them
+    // (EXACT: all with the online rescale).
+    auto pass = [&](auto exact_tag, const auto &qq, auto &mm, auto &ll, auto &aa) __attribute__((always_inline)) {
         constexpr bool EXACT = decltype(exact_tag)::value;
+        constexpr int NQ = sizeof(mm) / sizeof(float);
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            m[qb] = -INFINITY;
-            l[qb] = 0.0f;
+        for (int qb = 0; qb < NQ; ++qb) {
+            mm[qb] = -INFINITY;
+            ll[qb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int db = 0; db < 8; ++db)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[qb][db][i] = 0.0f;
+                for (int i = 0; i < 4; ++i) aa[qb][db][i] = 0.0f;
         }
         dma_tile(krs, kvoff, t0 * kstep, lds_k0);
         dma_tile(vrs, vvoff, t0 * vstep, lds_v0);
@@ -922,9 +932,9 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
             dma_tile(krs, kvoff, (tile + 1) * kstep, kn);
             dma_tile(vrs, vvoff, (tile + 1) * vstep, vn);
             if constexpr (EXACT || decltype(first_tag)::value)
-                exact_tile16<false, NEG>(kc, vc, kBN, qreg, kidx, vidx, g, c, m, l, acc);
+                exact_tile16<false, NEG>(kc, vc, kBN, qq, kidx, vidx, g, c, mm, ll, aa);
             else
-                ref_tile16<false>(kc, vc, kBN, qreg, kidx, vidx, g, c, m, l, acc);
+                ref_tile16<false>(kc, vc, kBN, qq, kidx, vidx, g, c, mm, ll, aa);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         };
@@ -941,24 +951,24 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
                 const bf16_t *kc = odd ? lds_k1 : lds_k0;
                 const bf16_t *vc = odd ? lds_v1 : lds_v0;
                 if constexpr (EXACT)
-                    exact_tile16<true, NEG>(kc, vc, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                    exact_tile16<true, NEG>(kc, vc, valid_last, qq, kidx, vidx, g, c, mm, ll, aa);
                 else
-                    ref_tile16<true>(kc, vc, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                    ref_tile16<true>(kc, vc, valid_last, qq, kidx, vidx, g, c, mm, ll, aa);
             }
         } else if (partial) {  // the partial tile is the only one
-            exact_tile16<true, NEG>(lds_k0, lds_v0, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+            exact_tile16<true, NEG>(lds_k0, lds_v0, valid_last, qq, kidx, vidx, g, c, mm, ll, aa);
         }
     };
-    pass(std::false_type{});
+    pass(std::false_type{}, qreg, m, l, acc);
     // Overflow against the reference maxima: redo the unit with the running
-    // maximum. The test covers the folded denominator (four finite partial
-    // sums can add up to +inf) and every accumulator. A key piece is held to
+    // maximum. The test covers the denominator (finite weights can sum to
+    // +inf) and every accumulator. A key piece is held to
     // FLT_MAX / kMaxSplit, so that the merge's sums over up to kMaxSplit
     // pieces, each weighted by at most 1, stay finite. Every wave has passed
     // its last LDS read of the pass before the barrier.
     float lt[2];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) lt[qb] = fold_groups_sum(l[qb]);
+    for (int qb = 0; qb < 2; ++qb) lt[qb] = den_total(l[qb]);
     const float limit = piece >= 0 ? __FLT_MAX__ / kMaxSplit : INFINITY;
     // x < limit is false for NaN, so NaN counts as overflow too.
     bool finite = lt[0] < limit && lt[1] < limit;
@@ -975,9 +985,20 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) any_bad |= wave_overflow[w];
     if (any_bad) {
-        pass(std::true_type{});
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) lt[qb] = fold_groups_sum(l[qb]);
+        // The fallback takes one query block at a time, with its Q operands
+        // loaded again, so that it holds half the state of the pass above
+        // (the kernel's register peak otherwise).
+        auto redo = [&](auto qb_tag) __attribute__((always_inline)) {
+            constexpr int qb = decltype(qb_tag)::value;
+            bf16x8_t q1[1][4];
+            load_q16(a, qbase, q_first, qb, l16, g, q1[0]);
+            pass(std::true_type{}, q1, *reinterpret_cast<float(*)[1]>(&m[qb]), *reinterpret_cast<f32x4_t(*)[1]>(&l[qb]),
+                 *reinterpret_cast<f32x4_t(*)[1][8]>(&acc[qb]));
+            lt[qb] = den_total(l[qb]);
+        };
+        redo(std::integral_constant<int, 0>{});
+        __syncthreads();  // every wave past its last LDS read
+        redo(std::integral_constant<int, 1>{});
     }
     if constexpr (SPLIT) {
         if (piece >= 0) {  // a piece: O, m and l of its 256 queries go to the workspace
@@ -1047,24 +1068,7 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         // query 16 qb + l16 of this wave's queries.
         bf16x8_t qreg[NQB][4];
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-            int query = q_first + 16 * qb + l16;
-            query = query < a.Sq ? query : a.Sq - 1;
-            const bf16_t *qrow = qbase + static_cast<int64_t>(query) * a.qs[2];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) qreg[qb][ks] = as_bf16x8(*reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * g));
-            if (a.prescale) {  // bf16(fp32(c) * fp32(q)) (tools/h3_attention.py:88)
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const uint4 u = __builtin_bit_cast(uint4, qreg[qb][ks]);
-                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-                    uint32_t o[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = pack2(lo2f(w[e]) * a.c, hi2f(w[e]) * a.c);
-                    qreg[qb][ks] = as_bf16x8(make_uint4(o[0], o[1], o[2], o[3]));
-                }
-            }
-        }
+        for (int qb = 0; qb < NQB; ++qb) load_q16(a, qbase, q_first, qb, l16, g, qreg[qb]);
 
         const __amdgpu_buffer_rsrc_t krs =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(kbase), static_cast<short>(0), a.k_bytes, kBufferWord3);
@@ -1091,19 +1095,21 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
         const int valid_last = a.Sk - full * kBN;
 
         f32x4_t acc[NQB][8];
-        float m[NQB], l[NQB];
-        // One pass over the unit's tiles: the first exact (it sets the reference
-        // maxima), the rest against them (EXACT: all with the online rescale).
-        auto pass = [&](auto exact_tag) __attribute__((always_inline)) {
+        float m[NQB];
+        f32x4_t l[NQB];
+        // One pass over the unit's tiles for the query blocks of qq (see
+        // attention16_kernel).
+        auto pass = [&](auto exact_tag, const auto &qq, auto &mm, auto &ll, auto &aa) __attribute__((always_inline)) {
             constexpr bool EXACT = decltype(exact_tag)::value;
+            constexpr int NQ = sizeof(mm) / sizeof(float);
 #pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) {
-                m[qb] = -INFINITY;
-                l[qb] = 0.0f;
+            for (int qb = 0; qb < NQ; ++qb) {
+                mm[qb] = -INFINITY;
+                ll[qb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[qb][db][i] = 0.0f;
+                    for (int i = 0; i < 4; ++i) aa[qb][db][i] = 0.0f;
             }
             dma_tile(krs, kvoff, t0 * kstep, lds_k0);
             dma_tile(vrs, vvoff, t0 * vstep, lds_v0);
@@ -1116,9 +1122,9 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
                 dma_tile(krs, kvoff, (tile + 1) * kstep, kn);
                 dma_tile(vrs, vvoff, (tile + 1) * vstep, vn);
                 if constexpr (EXACT || decltype(first_tag)::value)
-                    exact_tile16<false, NEG>(kc, vc, kBN, qreg, kidx, vidx, g, c, m, l, acc);
+                    exact_tile16<false, NEG>(kc, vc, kBN, qq, kidx, vidx, g, c, mm, ll, aa);
                 else
-                    ref_tile16<false>(kc, vc, kBN, qreg, kidx, vidx, g, c, m, l, acc);
+                    ref_tile16<false>(kc, vc, kBN, qq, kidx, vidx, g, c, mm, ll, aa);
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
             };
@@ -1135,20 +1141,20 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
                     const bf16_t *kc = odd ? lds_k1 : lds_k0;
                     const bf16_t *vc = odd ? lds_v1 : lds_v0;
                     if constexpr (EXACT)
-                        exact_tile16<true, NEG>(kc, vc, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                        exact_tile16<true, NEG>(kc, vc, valid_last, qq, kidx, vidx, g, c, mm, ll, aa);
                     else
-                        ref_tile16<true>(kc, vc, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                        ref_tile16<true>(kc, vc, valid_last, qq, kidx, vidx, g, c, mm, ll, aa);
                 }
             } else if (partial) {  // the partial tile is the only one
-                exact_tile16<true, NEG>(lds_k0, lds_v0, valid_last, qreg, kidx, vidx, g, c, m, l, acc);
+                exact_tile16<true, NEG>(lds_k0, lds_v0, valid_last, qq, kidx, vidx, g, c, mm, ll, aa);
             }
         };
-        pass(std::false_type{});
+        pass(std::false_type{}, qreg, m, l, acc);
         // Overflow against the reference maxima: redo the unit with the running
         // maximum (as attention16_kernel does).
         float lt[NQB];
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) lt[qb] = fold_groups_sum(l[qb]);
+        for (int qb = 0; qb < NQB; ++qb) lt[qb] = den_total(l[qb]);
         constexpr float limit = INFINITY;
         // x < limit is false for NaN, so NaN counts as overflow too.
         bool finite = true;
@@ -1167,9 +1173,20 @@ __global__ __launch_bounds__(kThreadsWG) __attribute__((amdgpu_waves_per_eu(kWav
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) any_bad |= wave_overflow[w];
         if (any_bad) {
-            pass(std::true_type{});
-#pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) lt[qb] = fold_groups_sum(l[qb]);
+            // One query block at a time, as attention16_kernel does. Every
+            // wave runs two passes, so that all reach the same barriers: a
+            // wave of one block computes it twice (the same result).
+            auto redo = [&](auto qb_tag) __attribute__((always_inline)) {
+                constexpr int qb = decltype(qb_tag)::value;
+                bf16x8_t q1[1][4];
+                load_q16(a, qbase, q_first, qb, l16, g, q1[0]);
+                pass(std::true_type{}, q1, *reinterpret_cast<float(*)[1]>(&m[qb]),
+                     *reinterpret_cast<f32x4_t(*)[1]>(&l[qb]), *reinterpret_cast<f32x4_t(*)[1][8]>(&acc[qb]));
+                lt[qb] = den_total(l[qb]);
+            };
+            redo(std::integral_constant<int, 0>{});
+            __syncthreads();  // every wave past its last LDS read
+            redo(std::integral_constant<int, NQB - 1>{});
         }
         // o = acc / denominator, bf16: lane l holds dims 16 db + 4 g .. +4 of
         // query 16 qb + l16.

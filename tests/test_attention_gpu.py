@@ -418,9 +418,9 @@ def _dominant_keys(Sk, keys, logit_log2, v_value):
 def test_attention_folded_denominator_overflow_falls_back(pkg, oracle, device):
     """Four keys of one later tile, one in each 16-lane group of the lanes
     that hold a query's keys (tile offsets 0, 4, 8, 12), each 127 log2 units
-    above the first tile's maximum: every lane's partial denominator (2^127)
-    and every accumulator (4 * 2^127 * 0.25) stays finite, but the folded
-    denominator (2^129) overflows. The unit must take the exact fallback and
+    above the first tile's maximum: every weight (2^127) and every
+    accumulator (4 * 2^127 * 0.25) stays finite, but their sum, the
+    denominator (2^129), overflows. The unit must take the exact fallback and
     give about 0.25 everywhere, not o = 0."""
     keys = [320, 324, 328, 332]
     q, k, v = _dominant_keys(700, keys, 127.0, 0.25)
