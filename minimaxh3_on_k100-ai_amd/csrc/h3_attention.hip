@@ -658,15 +658,16 @@ __device__ __forceinline__ void qk_tile16(const bf16_t *kt, const bf16x8_t (&qre
             for (int qb = 0; qb < NQB; ++qb)
                 s[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qreg[qb][ks], s[qb][kb], 0, 0, 0);
         }
-    // Rolling window of K operand reads, three ahead of the MFMAs (measured
-    // +1.3% over two ahead; four or five ahead, or a deeper V^T window, lost).
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    // Rolling window of K operand reads, four ahead of the MFMAs (measured
+    // +0.8% over three ahead, which was +1.3% over two; five ahead, or a
+    // deeper V^T window, lose).
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 13; ++i) {
+    for (int i = 0; i < 12; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 3 * NQB, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NQB, 0);
 }
 
 // P = bf16(exp2(c s - m)) (keys >= valid: 0 when MASK), the denominator
