@@ -193,15 +193,18 @@ def test_qkv_pack_fp8_codes(pkg, oracle, device, T, P, Hs):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,P,Hs", [(1024, 2, 7), (8192, 1, 14), (77, 4, 3), (5, 1, 1)],
-                         ids=["1024x2x7", "8192x1x14", "77x4x3", "5x1x1"])
+@pytest.mark.parametrize("T,P,Hs", [(1024, 2, 7), (8192, 1, 14), (77, 4, 3), (5, 1, 1), (1, 4, 33)],
+                         ids=["1024x2x7", "8192x1x14", "77x4x3", "5x1x1", "1x4x33-fewer-batches-than-heads"])
 def test_qkv_pack_fp8_vamax(pkg, oracle, device, T, P, Hs):
     """The pack with V's amax folded into slots: q8 / k8 / v / descales as the
     plain fp8 pack, the maximum over each head's slots equals the oracle's
     amax of |v| over that head's rows, and V quantised from the slots equals
     the oracle's per-head quantisation bitwise (codes and descales), in the
     V^T layout the fp8 attention reads. One head gets a large outlier so its
-    amax is a single element somewhere in the middle of the rows."""
+    amax is a single element somewhere in the middle of the rows. Launches
+    with at least one V block per head pin V's blocks to heads (their own
+    kernel instantiation); 1x4x33 has 9 batches of 16 rows for 132 heads and
+    takes the other path (V's maxima folded in LDS, then atomically)."""
     projected, wq, wk, cache, positions = _case(T, P, Hs, 7 * T + P, device)
     projected[T // 2, 2, P * Hs - 1, 17] = -37.0
     q, k, v = pkg.qkv_by_rank(projected, P)
@@ -235,7 +238,8 @@ def test_qkv_pack_fp8_vamax(pkg, oracle, device, T, P, Hs):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,P,Hs", [(1024, 2, 7), (8192, 1, 14), (77, 4, 3)], ids=["1024x2x7", "8192x1x14", "77x4x3"])
+@pytest.mark.parametrize("T,P,Hs", [(1024, 2, 7), (8192, 1, 14), (77, 4, 3), (1, 4, 33)],
+                         ids=["1024x2x7", "8192x1x14", "77x4x3", "1x4x33-fewer-batches-than-heads"])
 def test_qkv_pack_fp8x2_vamax(pkg, oracle, device, T, P, Hs):
     """The pack with two-term q and k codes: hi codes, lo codes and descales
     bitwise equal to the oracle's qkv_norm_rope_pack_fp8_two_term (the hi
