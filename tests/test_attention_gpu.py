@@ -415,6 +415,36 @@ def _dominant_keys(Sk, keys, logit_log2, v_value):
     return q.to(BF), k.to(BF), v.to(BF)
 
 
+def test_attention_dominated_rows_are_exact(pkg, oracle, device):
+    """One key of a later tile dominates every query (about 50 log2 units
+    above the first tile's logits, which set the reference maximum), and its
+    V row is 1.96875 in every dim. The weight p of that key is a power of two
+    far from 1, so bf16(p) differs from p by a quarter of a percent or more
+    (the key value is chosen so): a denominator that summed the fp32 p would
+    leave o = 1.96875 (1 + delta), which rounds to the next bf16 value. The
+    kernel's denominator sums the same bf16 weights that multiply V, so o is
+    the V row exactly, in every query and dim, as the fp64 reference's is."""
+    c = torch.tensor(128 ** -0.5 * math.log2(math.e), dtype=torch.float32)
+    pick = None
+    for kval in torch.arange(20.0, 30.0, 0.125):  # bf16-exact key values
+        p = torch.exp2(c * (16.0 * kval.to(torch.float32)))
+        delta = float((p.to(BF).float() - p).abs() / p)
+        if delta >= 2.5e-3:
+            pick = float(kval)
+            break
+    assert pick is not None
+    key, v_dom = 333, 1.96875
+    q, k, v = _dominant_keys(700, [key], 1.0, v_dom)
+    k[0, 0, key, 0] = pick
+    assert float(k[0, 0, key, 0]) == pick and float(v[0, 0, key, 5]) == v_dom
+    out = torch.full(q.shape, float("nan"), dtype=BF, device=device)
+    pkg.make_attention(split_last_round=False)(q.to(device), k.to(device), v.to(device), 128 ** -0.5, out)
+    torch.cuda.synchronize()
+    want = oracle.attention(q.double(), k.double(), v.double(), 128 ** -0.5)
+    assert torch.equal(want.to(BF), torch.full_like(want, v_dom).to(BF))
+    assert torch.equal(out.cpu(), torch.full(q.shape, v_dom, dtype=BF)), int((out.cpu() != v_dom).sum())
+
+
 def test_attention_folded_denominator_overflow_falls_back(pkg, oracle, device):
     """Four keys of one later tile, one in each 16-lane group of the lanes
     that hold a query's keys (tile offsets 0, 4, 8, 12), each 127 log2 units
