@@ -434,8 +434,8 @@ def bench_pointwise(pkg, device) -> dict:
 def cpu_host() -> dict:
     """The host CPU the CPU figures run on: its model, the CPUs the OS reports
     and the ones this process may run on, and torch's thread count (the
-    threads every CPU figure uses: the GPU box grants a job a share of its
-    CPUs and sets OMP_NUM_THREADS to it, which torch follows)."""
+    threads every CPU figure uses: a host that grants a job a share of its
+    CPUs sets OMP_NUM_THREADS to it, which torch follows)."""
     model = platform.processor() or "unknown"
     try:
         with open("/proc/cpuinfo") as f:

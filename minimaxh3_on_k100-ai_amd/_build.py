@@ -19,7 +19,7 @@ LIBRARY = PACKAGE_DIR / "libh3mi355x.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (some of
-# their forms have given silently wrong results on these boxes).
+# their forms have produced intermittent, silently wrong results on MI355X).
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -1,6 +1,6 @@
 """GPU parity of the bf16 attention kernel.
 
-Bar (north star): max |err| <= 2e-2 and relative RMS <= 1e-2 against an fp32
+Bar (the operator's tolerance): max |err| <= 2e-2 and relative RMS <= 1e-2 against an fp32
 (or fp64) softmax(q k^T s) v reference. Small and ragged shapes are checked
 against the fp64 CPU oracle; the S = 8192 and S = 73,984 configurations
 against a chunked fp32 reference computed on the GPU with torch (fp32 matmul)
