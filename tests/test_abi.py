@@ -8,6 +8,7 @@ from __future__ import annotations
 import ctypes
 import re
 import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -422,6 +423,36 @@ def test_noalloc_pack_face_rejects_what_it_cannot_take(pkg):
         call(2, 1, 1025)
     with pytest.raises(ValueError, match="int64 positions"):
         call(4, 1, 3, torch.int32)
+
+
+def test_missing_library_raises_for_every_entry_point(tmp_path):
+    """Without libh3mi355x.so every entry point raises ImportError (in a fresh
+    interpreter, whose library path names a file that does not exist): the
+    package has no non-HIP path to fall back to."""
+    code = (
+        "import importlib, sys\n"
+        "from pathlib import Path\n"
+        f"sys.path.insert(0, {str(ROOT)!r})\n"
+        "L = importlib.import_module('minimaxh3_on_k100-ai_amd._lib')\n"
+        f"L.LIBRARY_PATH = Path({str(tmp_path / 'absent.so')!r})\n"
+        "names = sorted(L.ENTRY_POINTS)\n"
+        "for name in names:\n"
+        "    try:\n"
+        "        L.entry(name)\n"
+        "    except ImportError as e:\n"
+        "        assert 'no non-HIP fallback' in str(e), e\n"
+        "        continue\n"
+        "    raise SystemExit('no error for ' + name)\n"
+        "try:\n"
+        "    L.attention_workspace_bytes(1, 1, 1, 1)\n"
+        "    raise SystemExit('no error for the workspace query')\n"
+        "except ImportError:\n"
+        "    pass\n"
+        "print('raised for', len(names))\n"
+    )
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert f"raised for {len(declared_entry_points())}" in r.stdout, r.stdout
 
 
 def test_raw_qk_norm_rope_form_is_twelve_arguments(pkg):
