@@ -155,16 +155,16 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
-// fp32 -> bf16 -> fp32, i.e. the value `.to(bfloat16)` leaves behind.
-__device__ __forceinline__ float rbf(float a) {
-    return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) << 16);
-}
+// fp32 -> bf16 -> fp32, i.e. the value `.to(bfloat16)` leaves behind, in one
+// instruction: the packed conversion of (0, a) puts bf16(a) in the high half
+// over a zero low half, which read as fp32 is exactly bf16(a).
+__device__ __forceinline__ float rbf(float a) { return __uint_as_float(pack2(0.0f, a)); }
 
-// Round a pair to bf16 and widen back (one packed conversion).
+// The same for a pair (two conversions: one conversion of the pair would need
+// a shift and a mask to widen its halves, three instructions for two values).
 __device__ __forceinline__ void rbf2(float &a, float &b) {
-    uint32_t p = pack2(a, b);
-    a = lo2f(p);
-    b = hi2f(p);
+    a = rbf(a);
+    b = rbf(b);
 }
 
 // 1/sqrt(v) with two IEEE roundings (correctly rounded sqrt, then correctly
