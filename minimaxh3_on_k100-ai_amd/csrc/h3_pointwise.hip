@@ -422,12 +422,12 @@ __device__ __forceinline__ void stage_vectors(const RmsArgs &a, int64_t b, int W
 //
 // EXACT: W8 = 64 G, so no group is clamped or masked; the row's addresses are
 // then one base and constant offsets, the kernel is held to 80 VGPRs (at
-// G = 14 one 8-byte value per lane goes to scratch across each row), and three
+// G = 14 it fits them without spilling), and three
 // 512-thread blocks share a CU (24 waves, 6144 rows in flight over the chip):
 // measured 46.5 against 49.5 us for the clamped form at two blocks per CU
 // (RMSNorm + AdaLN at [8192, 7168]). The EXACT kernel over 2 or 4 blocks per CU
 // measured 51 us; 16-byte aligned LDS reads of the staged rows (ds_read_b128
-// instead of ds_read2_b32 pairs) raise its spill to 284 bytes and cost 2.4x.
+// instead of ds_read2_b32 pairs) made it spill 284 bytes and cost 2.4x.
 template <int G, int MODE, int THREADS, bool EXACT>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(EXACT ? 6 : 1)))
 void rms_staged_kernel(RmsArgs a) {
