@@ -294,6 +294,54 @@ def test_head_rows_across_magnitudes(pkg, oracle, device, eps):
     assert_bitwise(outs[1], q_ref, "q/k/v pack (k)")
 
 
+def test_head_rows_special_values(pkg, oracle, device):
+    """Head rows holding +inf, -inf or NaN (the whole row's sum, and so every
+    channel, follows IEEE: inf * 0 = NaN), rows of bf16 subnormals, rows whose
+    squares overflow (2^70) and zero rows, through rotate-half, interleaved, q
+    and k in one launch (different rows in each) and the q/k/v pack, bitwise
+    against the oracle (NaN == NaN)."""
+    gen = _gen(57)
+    T, H = 64, 4
+    x = torch.randn(T, 1, H, 128, generator=gen)
+    x[1, 0, 0, 5] = float("inf")
+    x[2, 0, 1, 77] = float("-inf")
+    x[3, 0, 2, 100] = float("nan")
+    x[4, 0, 3] = torch.randn(128, generator=gen) * 2.0 ** -130  # bf16 subnormals
+    x[5, 0, 0] = torch.randn(128, generator=gen) * 2.0 ** 70  # squares overflow
+    x[6, 0, 1] = 0.0
+    x[7, 0, 2, 64:] = float("inf")  # the pass-through and rotated halves of one row
+    x = x.to(BF)
+    k = torch.flip(x, dims=(0,)).contiguous()  # the special rows at other tokens for k
+    w = _randn(gen, 128)
+    w2 = _randn(gen, 128)
+    table48, table64 = _randn(gen, T, 96), _randn(gen, T, 128)
+    xd, kd, wd, w2d = x.to(device), k.to(device), w.to(device), w2.to(device)
+    out = torch.empty_like(xd)
+    pkg.make_qk_norm_rope()(xd, wd, 1e-6, table48[:, :48].to(device), table48[:, 48:].to(device), out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.qk_norm_rope(x, w, 1e-6, table48[:, :48], table48[:, 48:]), "rotate-half")
+    c64, s64 = table64[:, :64], table64[:, 64:]
+    ref_q = oracle.qk_norm_rope_interleaved(x, w, 1e-6, c64, s64)
+    ref_k = oracle.qk_norm_rope_interleaved(k, w2, 1e-6, c64, s64)
+    out = torch.empty_like(xd)
+    pkg.make_qk_norm_rope_interleaved()(xd, wd, 1e-6, c64.to(device), s64.to(device), out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, ref_q, "interleaved")
+    qo, ko = torch.empty_like(xd), torch.empty_like(kd)
+    pkg.make_qk_norm_rope_interleaved_qk()(xd, kd, wd, w2d, 1e-6, c64.to(device), s64.to(device), qo, ko)
+    torch.cuda.synchronize()
+    assert_bitwise(qo, ref_q, "q of q + k")
+    assert_bitwise(ko, ref_k, "k of q + k")
+    outs = [torch.empty_like(xd) for _ in range(3)]
+    positions = torch.arange(T)
+    pkg.make_qkv_norm_rope_pack()(xd, kd, xd, wd, w2d, 1e-6, table48.to(device), positions.to(device), *outs)
+    torch.cuda.synchronize()
+    q_ref, k_ref, v_ref = oracle.qkv_norm_rope_pack(x, k, x, w, w2, 1e-6, table48, positions)
+    assert_bitwise(outs[0], q_ref, "q/k/v pack (q)")
+    assert_bitwise(outs[1], k_ref, "q/k/v pack (k)")
+    assert_bitwise(outs[2], v_ref, "q/k/v pack (v)")
+
+
 def test_qk_norm_rope_interleaved(pkg, oracle, device):
     q, k, w_q, w_k, pos = oracle.qk_norm_rope_inputs(T=2048, H=14, seed=3)
     cos, sin = oracle.rope_table_interleaved(pos)
