@@ -995,9 +995,10 @@ struct GatedResidualOp {
 
 // silu(g) = g / (1 + exp(-g)) in fp32, for |g| < 64, with the same values as
 // __fdiv_rn(g, 1 + expf(-g)) after the bf16 rounding that follows it. The
-// exponential is expf's own reduction (exp(x) = 2^n 2^t, n = rint(x log2 e),
-// t the remainder with log2 e split in two parts) without its overflow and
-// underflow selects, which cannot fire for |g| < 64. The quotient is
+// exponential is a Cody-Waite range reduction (Cody and Waite, 1980):
+// exp(x) = 2^n 2^t with n = rint(x log2 e) and t the remainder, log2 e split
+// into its fp32 value and the residual (constants fixed by the mathematics);
+// no overflow or underflow handling is needed for |g| < 64. The quotient is
 // q0 = g rcp(d) plus one residual correction. Every bf16 g with |g| < 64 takes
 // this path in the exhaustive swiglu test, whose bf16 results are bitwise the
 // oracle's.
